@@ -1,0 +1,260 @@
+// capi.cpp — the extern "C" boundary (include/ei_attn.h): argument validation, error
+// reporting and dispatch to the gfx950 launchers.  No exception leaves this file; every
+// entry point returns an EI_* status and records a message for ei_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/ei_attn.h"
+#include "launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return EI_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(EI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+#define REQUIRE(cond, ...)                           \
+    do {                                             \
+        if (!(cond)) return fail(EI_ERR_ARG, __VA_ARGS__); \
+    } while (0)
+
+int check_heads(int n_head, int n_head_kv, int head_dim) {
+    if (head_dim != 128)
+        return fail(EI_ERR_UNSUPPORTED, "head_dim %d: only 128 is built (the reference GPU path requires it too)",
+                    head_dim);
+    REQUIRE(n_head > 0 && n_head_kv > 0, "n_head (%d) and n_head_kv (%d) must be positive", n_head, n_head_kv);
+    REQUIRE(n_head % n_head_kv == 0, "n_head %d is not a multiple of n_head_kv %d", n_head, n_head_kv);
+    const int g = n_head / n_head_kv;
+    if (g != 1 && g != 2 && g != 4 && g != 8)
+        return fail(EI_ERR_UNSUPPORTED, "GQA group %d: built for 1, 2, 4, 8", g);
+    return EI_OK;
+}
+
+int check_rope(int rope_dim, int head_dim) {
+    REQUIRE(rope_dim > 0 && rope_dim % 2 == 0 && rope_dim <= head_dim, "rope_dim %d must be even and in (0, %d]",
+            rope_dim, head_dim);
+    return EI_OK;
+}
+
+}  // namespace
+
+#define EI_API extern "C" __attribute__((visibility("default")))
+
+EI_API const char* ei_last_error(void) { return g_err.c_str(); }
+
+EI_API int ei_abi_version(void) { return 1; }
+
+EI_API int ei_rope_table_fill(float* cs_host, int n_ctx, int rope_dim, double theta) {
+    REQUIRE(cs_host != nullptr, "cs_host is null");
+    REQUIRE(n_ctx > 0, "n_ctx %d must be positive", n_ctx);
+    REQUIRE(rope_dim > 0 && rope_dim % 2 == 0, "rope_dim %d must be even and positive", rope_dim);
+    REQUIRE(theta > 0.0, "theta must be positive");
+    const int half = rope_dim / 2;
+    for (int i = 0; i < half; ++i) {
+        const double inv = std::pow(theta, -2.0 * i / rope_dim);
+        for (int p = 0; p < n_ctx; ++p) {
+            const double th = double(p) * inv;
+            cs_host[(size_t(p) * half + i) * 2 + 0] = float(std::cos(th));
+            cs_host[(size_t(p) * half + i) * 2 + 1] = float(std::sin(th));
+        }
+    }
+    return ok();
+}
+
+EI_API int ei_headnorm_rope(ei_stream_t stream, float* buf, int rows, long row_stride, int n_heads, int head_dim,
+                            const float* gamma, const float* cs, const int* pos_dev, int rope_dim, float eps) {
+    if (head_dim != 128) return fail(EI_ERR_UNSUPPORTED, "head_dim %d: only 128 is built", head_dim);
+    if (int e = check_rope(rope_dim, head_dim)) return e;
+    REQUIRE(buf && gamma && cs && pos_dev, "null pointer argument");
+    REQUIRE(rows >= 0 && n_heads > 0, "rows %d / n_heads %d", rows, n_heads);
+    REQUIRE(row_stride >= (long)n_heads * head_dim, "row_stride %ld < n_heads*head_dim", row_stride);
+    if (rows == 0) return ok();
+    return hip_status(ei::launch_headnorm_rope(static_cast<hipStream_t>(stream), buf, rows, row_stride, n_heads,
+                                               gamma, cs, pos_dev, rope_dim, eps),
+                      "ei_headnorm_rope launch");
+}
+
+EI_API int ei_kv_append(ei_stream_t stream, const float* k_src, const float* v_src, long src_stride, int rows,
+                        float* kc, float* vc, int kd, const int* pos_dev) {
+    REQUIRE(k_src && v_src && kc && vc && pos_dev, "null pointer argument");
+    REQUIRE(rows >= 0, "rows %d", rows);
+    REQUIRE(kd > 0 && kd % 4 == 0, "kd %d must be a positive multiple of 4", kd);
+    REQUIRE(src_stride % 4 == 0 && src_stride >= kd, "src_stride %ld must be a multiple of 4 and >= kd", src_stride);
+    REQUIRE(aligned16(k_src) && aligned16(v_src) && aligned16(kc) && aligned16(vc), "pointers must be 16-byte aligned");
+    if (rows == 0) return ok();
+    return hip_status(ei::launch_kv_append(static_cast<hipStream_t>(stream), k_src, v_src, src_stride, rows, kc, vc,
+                                           kd, pos_dev),
+                      "ei_kv_append launch");
+}
+
+EI_API int ei_qkv_prepare(ei_stream_t stream, float* qkv, int rows, long row_stride, int n_head, int n_head_kv,
+                          int head_dim, const float* q_gamma, const float* k_gamma, const float* cs,
+                          const int* pos_dev, int rope_dim, float eps, float* kc, float* vc) {
+    if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
+    if (int e = check_rope(rope_dim, head_dim)) return e;
+    REQUIRE(qkv && q_gamma && k_gamma && cs && pos_dev && kc && vc, "null pointer argument");
+    REQUIRE(rows >= 0, "rows %d", rows);
+    REQUIRE(row_stride >= (long)(n_head + 2 * n_head_kv) * head_dim, "row_stride %ld < (H+2*HKV)*head_dim",
+            row_stride);
+    if (rows == 0) return ok();
+    return hip_status(ei::launch_qkv_prepare(static_cast<hipStream_t>(stream), qkv, rows, row_stride, n_head,
+                                             n_head_kv, q_gamma, k_gamma, cs, pos_dev, rope_dim, eps, kc, vc),
+                      "ei_qkv_prepare launch");
+}
+
+EI_API size_t ei_attn_decode_ws_bytes(int n_seq, int n_head, int n_head_kv, int max_kv) {
+    if (n_seq <= 0 || n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv || max_kv <= 0) return 0;
+    return ei::decode_ws_bytes(n_seq, n_head, n_head_kv, max_kv);
+}
+
+EI_API int ei_attn_workspace_init(ei_stream_t stream, void* ws, size_t ws_bytes) {
+    REQUIRE(ws != nullptr, "workspace is null");
+    REQUIRE(aligned16(ws), "workspace must be 16-byte aligned");
+    return hip_status(ei::launch_ws_clear(static_cast<hipStream_t>(stream), ws, ws_bytes), "workspace clear");
+}
+
+namespace {
+
+int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void* ws, size_t ws_bytes, bool fused) {
+    REQUIRE(max_kv > 0, "max_kv %d must be positive", max_kv);
+    REQUIRE(ws != nullptr && aligned16(ws), "workspace missing or not 16-byte aligned");
+    const size_t need = ei::decode_ws_bytes(n_seq, a.H, a.HKV, max_kv);
+    REQUIRE(ws_bytes >= need, "workspace of %zu bytes < %zu needed (ei_attn_decode_ws_bytes)", ws_bytes, need);
+    const ei::DecodePlan p = ei::decode_plan(n_seq, a.HKV, max_kv);
+    const size_t slots = (size_t)n_seq * a.HKV * p.nsplit;
+    const int G = a.H / a.HKV;
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    char* base = static_cast<char*>(ws);
+    a.part_acc = reinterpret_cast<float*>(base);
+    a.part_ml = reinterpret_cast<float*>(base + al(slots * G * 128 * 4));
+    a.counters = reinterpret_cast<unsigned*>(base + al(slots * G * 128 * 4) + al(slots * G * 2 * 4));
+    a.chunk = p.chunk;
+    a.nsplit = p.nsplit;
+    return hip_status(ei::launch_decode(st, a, n_seq, fused), "decode launch");
+}
+
+}  // namespace
+
+EI_API int ei_attn_decode(ei_stream_t stream, const float* q, float* out, const float* kc, const float* vc,
+                          const int* pos_dev, int n_head, int n_head_kv, int head_dim, float scale, int max_kv,
+                          void* ws, size_t ws_bytes) {
+    if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
+    REQUIRE(q && out && kc && vc && pos_dev, "null pointer argument");
+    REQUIRE(aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc), "pointers must be 16-byte aligned");
+    ei::DecodeArgs a{};
+    a.q = q;
+    a.q_stride = (long)n_head * head_dim;
+    a.kc = const_cast<float*>(kc);
+    a.vc = const_cast<float*>(vc);
+    a.pos_dev = pos_dev;
+    a.out = out;
+    a.H = n_head;
+    a.HKV = n_head_kv;
+    a.scale = scale;
+    return decode_common(static_cast<hipStream_t>(stream), a, 1, max_kv, ws, ws_bytes, false);
+}
+
+EI_API int ei_attn_decode_batched(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc,
+                                  const float* vc, const int64_t* kv_offset, const int* kv_len, int n_seq,
+                                  int n_head, int n_head_kv, int head_dim, float scale, int max_kv, void* ws,
+                                  size_t ws_bytes) {
+    if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
+    REQUIRE(q && out && kc && vc && kv_offset && kv_len, "null pointer argument");
+    REQUIRE(n_seq > 0 && n_seq <= 65535, "n_seq %d out of range [1, 65535]", n_seq);
+    REQUIRE(q_stride >= (long)n_head * head_dim && q_stride % 4 == 0, "q_stride %ld", q_stride);
+    REQUIRE(aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc), "pointers must be 16-byte aligned");
+    ei::DecodeArgs a{};
+    a.q = q;
+    a.q_stride = q_stride;
+    a.kc = const_cast<float*>(kc);
+    a.vc = const_cast<float*>(vc);
+    a.kv_offset = kv_offset;
+    a.kv_len = kv_len;
+    a.out = out;
+    a.H = n_head;
+    a.HKV = n_head_kv;
+    a.scale = scale;
+    return decode_common(static_cast<hipStream_t>(stream), a, n_seq, max_kv, ws, ws_bytes, false);
+}
+
+EI_API int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc, float* vc,
+                          const int64_t* kv_offset, const int* kv_len, const int* pos_dev, int n_seq, int n_head,
+                          int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma, const float* cs,
+                          int rope_dim, float eps, float scale, int max_kv, void* ws, size_t ws_bytes) {
+    if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
+    if (int e = check_rope(rope_dim, head_dim)) return e;
+    REQUIRE(qkv && out && kc && vc && q_gamma && k_gamma && cs, "null pointer argument");
+    REQUIRE(n_seq > 0 && n_seq <= 65535, "n_seq %d out of range [1, 65535]", n_seq);
+    REQUIRE(kv_len != nullptr || (pos_dev != nullptr && n_seq == 1),
+            "either kv_len, or pos_dev with n_seq == 1, must be given");
+    REQUIRE(n_seq == 1 || kv_offset != nullptr, "kv_offset is required when n_seq > 1");
+    REQUIRE(row_stride >= (long)(n_head + 2 * n_head_kv) * head_dim, "row_stride %ld < (H+2*HKV)*head_dim",
+            row_stride);
+    REQUIRE(aligned16(qkv) && aligned16(out) && aligned16(kc) && aligned16(vc) && row_stride % 4 == 0,
+            "pointers and row_stride must be 16-byte aligned");
+    ei::DecodeArgs a{};
+    a.q = qkv;
+    a.q_stride = row_stride;
+    a.kc = kc;
+    a.vc = vc;
+    a.kv_offset = kv_offset;
+    a.kv_len = kv_len;
+    a.pos_dev = pos_dev;
+    a.out = out;
+    a.H = n_head;
+    a.HKV = n_head_kv;
+    a.scale = scale;
+    a.q_gamma = q_gamma;
+    a.k_gamma = k_gamma;
+    a.cs = reinterpret_cast<const float2*>(cs);
+    a.rope_dim = rope_dim;
+    a.eps = eps;
+    return decode_common(static_cast<hipStream_t>(stream), a, n_seq, max_kv, ws, ws_bytes, true);
+}
+
+EI_API int ei_attn_prefill(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc,
+                           const float* vc, const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim,
+                           float scale) {
+    if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
+    REQUIRE(q && out && kc && vc && pos_dev, "null pointer argument");
+    REQUIRE(B >= 0, "B %d", B);
+    REQUIRE(q_stride >= (long)n_head * head_dim && q_stride % 4 == 0, "q_stride %ld", q_stride);
+    REQUIRE(aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc), "pointers must be 16-byte aligned");
+    if (B == 0) return ok();
+    return hip_status(ei::launch_prefill(static_cast<hipStream_t>(stream), q, q_stride, out, kc, vc, pos_dev, B,
+                                         n_head, n_head_kv, scale),
+                      "prefill launch");
+}
+
+EI_API int ei_synth_fill(ei_stream_t stream, float* dst, size_t n, uint64_t seed, uint64_t offset, long row_len,
+                         long spike_every, float spike_mult) {
+    REQUIRE(dst != nullptr || n == 0, "dst is null");
+    REQUIRE(row_len > 0, "row_len %ld must be positive", row_len);
+    return hip_status(ei::launch_synth_fill(static_cast<hipStream_t>(stream), dst, n, seed, offset, row_len,
+                                            spike_every, spike_mult),
+                      "synth fill launch");
+}

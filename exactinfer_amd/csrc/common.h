@@ -1,0 +1,143 @@
+// common.h — shared device helpers for the gfx950 attention kernels.
+//
+// Wave64 lane exchanges: DPP for partners inside a row of 16 lanes, ds_swizzle (bit mode,
+// no LDS memory access) for partners 4 and 16 lanes away, and a bpermute for the half-wave
+// exchange.  All helpers are exact data moves; reductions built from them are
+// deterministic for a given launch shape.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace ei {
+
+constexpr int kHeadDim = 128;  // Qwen3 head_dim; every kernel is specialised for it
+
+// ------------------------------------------------------------------ lane exchanges
+__device__ __forceinline__ float lane_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));  // quad_perm 1,0,3,2
+}
+__device__ __forceinline__ float lane_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));  // quad_perm 2,3,0,1
+}
+__device__ __forceinline__ float lane_xor4(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));  // and 0x1F, xor 4
+}
+__device__ __forceinline__ float lane_xor8(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));  // row_ror:8
+}
+__device__ __forceinline__ float lane_xor16(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // and 0x1F, xor 16
+}
+__device__ __forceinline__ float lane_xor32(float v) { return __shfl_xor(v, 32); }
+
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+    if constexpr (M == 1) return lane_xor1(v);
+    else if constexpr (M == 2) return lane_xor2(v);
+    else if constexpr (M == 4) return lane_xor4(v);
+    else if constexpr (M == 8) return lane_xor8(v);
+    else if constexpr (M == 16) return lane_xor16(v);
+    else return lane_xor32(v);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, lane_xor1(v));
+    v = fmaxf(v, lane_xor2(v));
+    v = fmaxf(v, lane_xor4(v));
+    v = fmaxf(v, lane_xor8(v));
+    v = fmaxf(v, lane_xor16(v));
+    return fmaxf(v, lane_xor32(v));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v += lane_xor1(v);
+    v += lane_xor2(v);
+    v += lane_xor4(v);
+    v += lane_xor8(v);
+    v += lane_xor16(v);
+    return v + lane_xor32(v);
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// ------------------------------------------------------------------ QK-norm + RoPE of one head
+// One wave normalises and rotates one 128-float head vector.
+//   ss  = sum of double(x)^2 (tree order; the value in double matches the sequential
+//         sum to ~1e-16 relative, so the float `inv` is the reference's except within an
+//         ulp-rounding tie)                                   src/ops.cpp:155-160
+//   inv = float(1 / sqrt(ss/128 + double(eps)));  y = (x * inv) * gamma
+//   NEOX rotation of halves with the table's (cos, sin):      src/model.cpp:23-32
+//   y[i] = a*c - b*s,  y[i+half] = a*s + b*c   (no FMA contraction: two products, then +/-)
+// `dst` is LDS scratch of 128 floats owned by this wave (may alias nothing else).
+// Returns in *o0 / *o1 the outputs for elements lane and lane+64.
+__device__ __forceinline__ void norm_rope_head(const float* __restrict__ src, const float* __restrict__ gamma,
+                                               const float2* __restrict__ cs_row, int rope_dim, float eps,
+                                               float* dst, int lane, float* o0, float* o1) {
+#pragma clang fp contract(off)
+    const float x0 = src[lane], x1 = src[lane + 64];
+    double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
+    ss = wave_sum_f64(ss);
+    const float inv = (float)(1.0 / sqrt(ss / (double)kHeadDim + (double)eps));
+    const float y0 = (x0 * inv) * gamma[lane];
+    const float y1 = (x1 * inv) * gamma[lane + 64];
+    dst[lane] = y0;
+    dst[lane + 64] = y1;
+    __builtin_amdgcn_wave_barrier();
+    const int half = rope_dim >> 1;
+    float r0 = y0, r1 = y1;
+    // element e: rotated if e < rope_dim; partner e+half (e < half) or e-half
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int e = lane + 64 * k;
+        float r = k == 0 ? y0 : y1;
+        if (e < rope_dim) {
+            if (e < half) {
+                const float2 t = cs_row[e];
+                const float a = r, b = dst[e + half];
+                const float acs = a * t.x, bsn = b * t.y;
+                r = acs - bsn;
+            } else {
+                const float2 t = cs_row[e - half];
+                const float a = dst[e - half], b = r;
+                const float asn = a * t.y, bcs = b * t.x;
+                r = asn + bcs;
+            }
+        }
+        if (k == 0) r0 = r;
+        else r1 = r;
+    }
+    __builtin_amdgcn_wave_barrier();
+    *o0 = r0;
+    *o1 = r1;
+}
+
+// ------------------------------------------------------------------ synthetic inputs
+// Counter-based N(0,1) (Irwin-Hall of twelve 16-bit uniforms from three splitmix64
+// outputs); integer arithmetic and an exact final conversion, identical on every platform.
+__host__ __device__ __forceinline__ uint64_t synth_mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__host__ __device__ __forceinline__ float synth_normal(uint64_t seed, uint64_t e) {
+    const uint64_t base = seed * 0xD1B54A32D192ED03ull + 3ull * e;
+    int64_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const uint64_t h = synth_mix64(base + (uint64_t)k);
+        s += (int64_t)(h & 0xFFFF) + (int64_t)((h >> 16) & 0xFFFF) + (int64_t)((h >> 32) & 0xFFFF) +
+             (int64_t)(h >> 48);
+    }
+    const int64_t n = s + 6 - 6 * 65536;
+    return (float)n * (1.0f / 65536.0f);
+}
+
+}  // namespace ei

@@ -1,0 +1,63 @@
+// launch.h — internal launchers behind the C ABI (capi.cpp validates, these launch).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace ei {
+
+// ------------------------------------------------------------------ prologue.hip
+hipError_t launch_headnorm_rope(hipStream_t st, float* buf, int rows, long row_stride, int n_heads,
+                                const float* gamma, const float* cs, const int* pos_dev, int rope_dim, float eps);
+hipError_t launch_kv_append(hipStream_t st, const float* k_src, const float* v_src, long src_stride, int rows,
+                            float* kc, float* vc, int kd, const int* pos_dev);
+hipError_t launch_qkv_prepare(hipStream_t st, float* qkv, int rows, long row_stride, int H, int HKV,
+                              const float* q_gamma, const float* k_gamma, const float* cs, const int* pos_dev,
+                              int rope_dim, float eps, float* kc, float* vc);
+hipError_t launch_synth_fill(hipStream_t st, float* dst, size_t n, uint64_t seed, uint64_t offset, long row_len,
+                             long spike_every, float spike_mult);
+
+// ------------------------------------------------------------------ decode.hip
+// Split plan: keys of one (sequence, kv head) are cut into `nsplit` chunks of `chunk`
+// keys (a multiple of the 64-key sub-tile); fixed by max_kv so graphs replay unchanged.
+struct DecodePlan {
+    int chunk;
+    int nsplit;
+};
+constexpr int kDecodeMaxSplits = 256;
+DecodePlan decode_plan(int n_seq, int HKV, int max_kv);
+size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv);
+
+struct DecodeArgs {
+    const float* q;         // raw [Q|K|V] row (fused) or normed q [H][128], per sequence
+    long q_stride;          // floats between sequences
+    float* kc;              // cache base (rows of HKV*128 floats)
+    float* vc;
+    const int64_t* kv_offset;  // per-sequence first cache row, or null (0)
+    const int* kv_len;         // per-sequence visible keys, or null (then *pos_dev + 1)
+    const int* pos_dev;
+    float* out;             // [n_seq][H][128]
+    int H, HKV;
+    float scale;
+    int chunk, nsplit;
+    float* part_acc;        // [n_seq*HKV*nsplit][G][128]
+    float* part_ml;         // [n_seq*HKV*nsplit][G][2]
+    unsigned* counters;     // [n_seq*HKV]
+    // fused prologue
+    const float* q_gamma;
+    const float* k_gamma;
+    const float2* cs;
+    int rope_dim;
+    float eps;
+};
+
+hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused);
+hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes);
+
+// ------------------------------------------------------------------ prefill.hip
+hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
+                          const float* vc, const int* pos_dev, int B, int H, int HKV, float scale);
+
+}  // namespace ei

@@ -1,0 +1,141 @@
+/*
+ * ei_attn.h — C ABI of the MI355X (gfx950) Qwen3 attention hot path.
+ *
+ * Conventions (mirroring the reference CUDA backend's, src/cuda/model_cuda.cu):
+ *  - Every entry point returns an int status: EI_OK (0) or an EI_ERR_* code; the message of
+ *    the last failure on the calling thread is returned by ei_last_error().  No C++
+ *    exception crosses this boundary (the reference throws std::runtime_error from CK/
+ *    CK_LAUNCH, src/cuda/model_cuda.cu:40-44; a C++ caller turns a non-zero status back
+ *    into that exception).
+ *  - All tensor pointers are device pointers owned by the caller; the library allocates
+ *    nothing.  `stream` is a hipStream_t (NULL = the default stream).  Launches are
+ *    asynchronous, perform no host synchronisation and are capturable into a hipGraph.
+ *  - Positions may live in device memory (`pos_dev`) so a captured graph replays
+ *    unchanged while the position advances (src/cuda/model_cuda.cu:1632, :1846).
+ *  - fp32 everywhere; head_dim must be 128 (the reference GPU path requires it,
+ *    src/cuda/model_cuda.cu:46, :1542); n_head must be a multiple of n_head_kv with a
+ *    group size of 1, 2, 4 or 8; rope_dim even and <= head_dim.
+ *  - KV cache layout per layer: [position][n_head_kv][head_dim] fp32 (src/model.cpp:153,
+ *    src/cuda/model_cuda.cu:1571), i.e. row p holds kd = n_head_kv*128 floats.
+ *  - Base pointers and row strides must be 16-byte aligned (multiples of 4 floats).
+ */
+#ifndef EI_ATTN_H
+#define EI_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ei_stream_t; /* hipStream_t */
+
+enum {
+    EI_OK = 0,
+    EI_ERR_ARG = 1,         /* invalid argument (shape, alignment, null pointer, size) */
+    EI_ERR_UNSUPPORTED = 2, /* valid in the reference but not built here (e.g. head_dim != 128) */
+    EI_ERR_HIP = 3          /* a HIP runtime call or kernel launch failed */
+};
+
+/* Message of the last failure on this thread ("" if none).  Valid until the next call. */
+const char* ei_last_error(void);
+
+/* ABI version, bumped on any signature change. */
+int ei_abi_version(void);
+
+/* ------------------------------------------------------------------ RoPE table
+ * Host-side fill of the (cos, sin) table the kernels read: cs[p][i] =
+ * (float(cos th), float(sin th)), th = double(p) * theta^(-2i/rope_dim) computed in double,
+ * shape [n_ctx][rope_dim/2][2].  Replaces the table build of src/cuda/model_cuda.cu:1610-1619
+ * (angles as in src/model.cpp:23-32 and rope_inv_freq, src/model.cpp:105-109).
+ * The caller copies it to device memory once. */
+int ei_rope_table_fill(float* cs_host, int n_ctx, int rope_dim, double theta);
+
+/* ------------------------------------------------------------------ QK-norm + RoPE
+ * In place on `rows` rows of `buf` (row b at buf + b*row_stride, head h at + h*128):
+ * per head, RMSNorm with gamma (sum of squares in double, inv = float(1/sqrt(ss/128+eps)),
+ * out = x*inv*gamma) then NEOX RoPE at position *pos_dev + b from `cs`.
+ * Replaces k_headnorm_rope (src/cuda/model_cuda.cu:87-105); arithmetic follows the CPU
+ * reference rmsnorm + rope (src/ops.cpp:155-160, src/model.cpp:23-32). */
+int ei_headnorm_rope(ei_stream_t stream, float* buf, int rows, long row_stride, int n_heads, int head_dim,
+                     const float* gamma, const float* cs, const int* pos_dev, int rope_dim, float eps);
+
+/* ------------------------------------------------------------------ KV append
+ * Bit-exact copy of `rows` K and V rows (kd floats each; row b at k_src + b*src_stride)
+ * into cache rows *pos_dev + b.  Rows outside [pos, pos+rows) are not touched.
+ * Replaces k_store_kv (src/cuda/model_cuda.cu:108-117) / src/model.cpp:186-189. */
+int ei_kv_append(ei_stream_t stream, const float* k_src, const float* v_src, long src_stride, int rows, float* kc,
+                 float* vc, int kd, const int* pos_dev);
+
+/* ------------------------------------------------------------------ fused prologue
+ * One launch for the per-layer prologue of src/cuda/model_cuda.cu:1800-1806 on a
+ * [rows][ (H + 2*HKV) * 128 ] QKV buffer ([Q | K | V] per row, row stride `row_stride`):
+ * QK-norm + RoPE of the H query heads and the HKV key heads in place (as
+ * ei_headnorm_rope), then K and V rows appended to the cache at *pos_dev + b
+ * (as ei_kv_append). */
+int ei_qkv_prepare(ei_stream_t stream, float* qkv, int rows, long row_stride, int n_head, int n_head_kv,
+                   int head_dim, const float* q_gamma, const float* k_gamma, const float* cs, const int* pos_dev,
+                   int rope_dim, float eps, float* kc, float* vc);
+
+/* ------------------------------------------------------------------ decode (split-K)
+ * Workspace for the decode entry points: per (sequence, kv head, key split) partial
+ * (m, l, acc) plus one arrival counter per (sequence, kv head).  max_kv bounds the number
+ * of visible keys of any sequence over the workspace's life (it fixes the split grid, so
+ * a captured graph stays valid as positions advance).  The workspace must be cleared once
+ * with ei_attn_workspace_init before first use; every decode call leaves it cleared
+ * again.  Calls that share a workspace must not overlap in time. */
+size_t ei_attn_decode_ws_bytes(int n_seq, int n_head, int n_head_kv, int max_kv);
+int ei_attn_workspace_init(ei_stream_t stream, void* ws, size_t ws_bytes);
+
+/* Single-sequence decode attention: q [n_head][128] (already normed + roped), cache rows
+ * 0..*pos_dev visible (T = *pos_dev + 1 <= max_kv), out [n_head][128].
+ * Replaces k_attn_split + k_attn_combine (src/cuda/model_cuda.cu:1043-1111); the math is
+ * the CPU reference's softmax attention (src/model.cpp:191-214). */
+int ei_attn_decode(ei_stream_t stream, const float* q, float* out, const float* kc, const float* vc,
+                   const int* pos_dev, int n_head, int n_head_kv, int head_dim, float scale, int max_kv, void* ws,
+                   size_t ws_bytes);
+
+/* Ragged multi-sequence decode: sequence s reads its q at q + s*q_stride ([n_head][128]),
+ * attends to cache rows kv_offset[s] .. kv_offset[s]+kv_len[s]-1 (kv_offset and kv_len
+ * are device arrays; 1 <= kv_len[s] <= max_kv) and writes out + s*n_head*128.
+ * No reference counterpart (the reference decodes one sequence); per sequence the
+ * result is that of ei_attn_decode. */
+int ei_attn_decode_batched(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc,
+                           const float* vc, const int64_t* kv_offset, const int* kv_len, int n_seq, int n_head,
+                           int n_head_kv, int head_dim, float scale, int max_kv, void* ws, size_t ws_bytes);
+
+/* Fused decode step: one launch doing ei_qkv_prepare + ei_attn_decode for one token per
+ * sequence.  qkv row s (at qkv + s*row_stride, [Q|K|V] raw projections) is read only;
+ * the normed+roped K row and the V row are written to cache row kv_offset[s] + pos_s,
+ * pos_s = kv_len[s]-1 (or *pos_dev when kv_len is NULL; then n_seq must be 1 and
+ * kv_offset may be NULL).  out [n_seq][n_head][128].  Equivalent to the per-layer
+ * sequence k_headnorm_rope(Q), k_headnorm_rope(K), k_store_kv, k_attn_split,
+ * k_attn_combine of src/cuda/model_cuda.cu:1800-1814. */
+int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc, float* vc,
+                   const int64_t* kv_offset, const int* kv_len, const int* pos_dev, int n_seq, int n_head,
+                   int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma, const float* cs,
+                   int rope_dim, float eps, float scale, int max_kv, void* ws, size_t ws_bytes);
+
+/* ------------------------------------------------------------------ causal prefill
+ * B query rows (row b at q + b*q_stride, heads [n_head][128], already normed + roped) at
+ * positions *pos_dev + b; query b attends to cache rows 0 .. *pos_dev + b (the whole
+ * chunk's K/V must already be appended).  out [B][n_head][128].  fp32 MFMA contraction
+ * with online softmax.  Replaces k_attn_prefill64 (src/cuda/model_cuda.cu:1204-1341);
+ * the math is the CPU reference's per-token attention (src/model.cpp:138-140, :191-214). */
+int ei_attn_prefill(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc, const float* vc,
+                    const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim, float scale);
+
+/* ------------------------------------------------------------------ synthetic inputs
+ * Not part of the reference path: fills n floats with the counter-based N(0,1)
+ * generator (element e = stream element offset+e of `seed`), multiplying by spike_mult
+ * every element whose row index ((offset+e) / row_len) is a multiple of spike_every
+ * (spike_every <= 0: no spikes).  Bit-identical to the CPU generator used by the tests. */
+int ei_synth_fill(ei_stream_t stream, float* dst, size_t n, uint64_t seed, uint64_t offset, long row_len,
+                  long spike_every, float spike_mult);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EI_ATTN_H */

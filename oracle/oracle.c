@@ -1,0 +1,342 @@
+/*
+ * oracle.c — CPU oracle for the Qwen3 attention hot path.  TEST INFRASTRUCTURE ONLY.
+ *
+ * This file is a plain-C restatement of the reference CPU path's arithmetic, used as the
+ * parity checker for the HIP kernels.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it.  The product path (exactinfer_amd/) never calls it.
+ *
+ * Build: gcc -O2 -ffp-contract=off (no contraction, no reassociation) so every float
+ * operation happens in the order the reference writes it (MSVC /fp:precise semantics of
+ * the reference build, CMakeLists.txt:49).  OpenMP only splits independent query heads,
+ * exactly like the reference (src/model.cpp:191), so results do not depend on thread count.
+ *
+ * Pinning of each function (what proves the restatement right, checked in tests/):
+ *   orc_rmsnorm          bit-exact vs the reference's own el::rmsnorm compiled from
+ *                        src/ops.cpp (oracle/_ref), + float64 closed form.
+ *   orc_rope_inv_freq,   bit-exact vs el::rope_inv_freq / el::rope compiled from
+ *   orc_rope             src/model.cpp (oracle/_ref), + rotation-norm invariant.
+ *   orc_rope_table       bit-exact vs orc_rope applied to unit vectors (the table is what
+ *                        src/cuda/model_cuda.cu:1610-1619 precomputes).
+ *   orc_kv_append        byte compare, untouched-row invariant.
+ *   orc_attn_decode      float64 brute force (orc_attn_f64) on small inputs; closed forms
+ *                        (1 key -> v0, identical keys -> mean V, dominant score -> that V);
+ *                        GQA == repeated K/V.  The reference attention loop sits inside
+ *                        CpuModel::forward, which needs a GGUF reader that does not build
+ *                        on Linux (src/gguf.cpp:12 includes <windows.h>), so it cannot be
+ *                        run directly.
+ *   orc_attn_split_combine  == single-pass orc_attn_decode within fp32 tolerance, and
+ *                        float64 brute force; empty-split rule.
+ *   orc_attn_f64         textbook softmax attention in double; checked by the closed forms.
+ *   orc_fill_normal      synthetic-input generator (not a reference function): exact
+ *                        integer arithmetic, checked for moments and against the GPU fill.
+ */
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_API __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------ synthetic inputs
+ * Counter-based generator shared with the GPU fill kernel: element e of stream `seed`
+ * is an Irwin-Hall(12) approximation of N(0,1) built from three splitmix64 outputs
+ * (twelve 16-bit uniforms).  All arithmetic is integer; the final int->float conversion
+ * and the multiply by 2^-16 are exact, so every platform produces identical bits. */
+static inline uint64_t orc_mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static inline float orc_normal_at(uint64_t seed, uint64_t e) {
+    const uint64_t base = seed * 0xD1B54A32D192ED03ull + 3ull * e;
+    int64_t s = 0;
+    for (int k = 0; k < 3; ++k) {
+        const uint64_t h = orc_mix64(base + (uint64_t)k);
+        s += (int64_t)(h & 0xFFFF) + (int64_t)((h >> 16) & 0xFFFF) + (int64_t)((h >> 32) & 0xFFFF) +
+             (int64_t)(h >> 48);
+    }
+    /* sum of 12 uniforms (h+0.5)/65536 minus 6, scaled by 65536: fits in 21 bits */
+    const int64_t n = s + 6 - 6 * 65536;
+    return (float)n * (1.0f / 65536.0f);
+}
+
+ORC_API void orc_fill_normal(float* out, size_t n, uint64_t seed, uint64_t offset) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_normal_at(seed, offset + i);
+}
+
+/* gamma ~ 1 + 0.1 * N(0,1), rounded step by step in float */
+ORC_API void orc_fill_gamma(float* out, size_t n, uint64_t seed) {
+    for (size_t i = 0; i < n; ++i) {
+        const float z = orc_normal_at(seed, i);
+        const float t = 0.1f * z;
+        out[i] = 1.0f + t;
+    }
+}
+
+/* ------------------------------------------------------------------ QK-norm
+ * src/ops.cpp:155-160: ss = sum double(x)^2 sequentially; inv = float(1/sqrt(ss/n + eps))
+ * (eps promoted to double); out = x * inv * w, two float multiplies left to right. */
+ORC_API void orc_rmsnorm(float* out, const float* x, const float* w, int n, float eps) {
+    double ss = 0.0;
+    for (int i = 0; i < n; ++i) ss += (double)x[i] * x[i];
+    const float inv = (float)(1.0 / sqrt(ss / n + eps));
+    for (int i = 0; i < n; ++i) {
+        const float t = x[i] * inv;
+        out[i] = t * w[i];
+    }
+}
+
+/* ------------------------------------------------------------------ RoPE
+ * src/model.cpp:105-109: inv_freq[i] = pow(base, -2.0*i/rope_dim) in double. */
+ORC_API void orc_rope_inv_freq(double* out, int rope_dim, double base) {
+    for (int i = 0; i < rope_dim / 2; ++i) out[i] = pow(base, -2.0 * i / rope_dim);
+}
+
+/* src/model.cpp:23-32: NEOX rotation of halves; angle th = pos*inv_freq[i] in double;
+ * cs = float(cos th), sn = float(sin th); v[i] = a*cs - b*sn, v[i+half] = a*sn + b*cs. */
+ORC_API void orc_rope(float* v, int pos, int dim, const double* inv_freq) {
+    const int half = dim / 2;
+    for (int i = 0; i < half; ++i) {
+        const double th = pos * inv_freq[i];
+        const float cs = (float)cos(th), sn = (float)sin(th);
+        const float a = v[i], b = v[i + half];
+        const float acs = a * cs, bsn = b * sn, asn = a * sn, bcs = b * cs;
+        v[i] = acs - bsn;
+        v[i + half] = asn + bcs;
+    }
+}
+
+/* src/cuda/model_cuda.cu:1610-1619: table cs[p][i] = (float(cos th), float(sin th)),
+ * th = double(p) * inv_freq[i], stored as interleaved pairs [n_ctx][rope_dim/2][2]. */
+ORC_API void orc_rope_table(float* cs, int n_ctx, int rope_dim, double base) {
+    const int half = rope_dim / 2;
+    double* inv = (double*)malloc(sizeof(double) * (size_t)(half > 0 ? half : 1));
+    orc_rope_inv_freq(inv, rope_dim, base);
+    for (int p = 0; p < n_ctx; ++p)
+        for (int i = 0; i < half; ++i) {
+            const double th = (double)p * inv[i];
+            cs[((size_t)p * half + i) * 2 + 0] = (float)cos(th);
+            cs[((size_t)p * half + i) * 2 + 1] = (float)sin(th);
+        }
+    free(inv);
+}
+
+/* Per-token QK-norm + RoPE over a block of rows, src/model.cpp:176-185: for row b (at
+ * position pos0+b) and each head h: rmsnorm(v, v, gamma, D, eps) then rope(v, pos, rope_dim).
+ * buf row b starts at buf + b*row_stride; head h at + h*D. */
+ORC_API void orc_headnorm_rope(float* buf, int rows, long row_stride, int n_heads, int D, const float* gamma,
+                               int pos0, int rope_dim, double base, float eps) {
+    double* inv = (double*)malloc(sizeof(double) * (size_t)(rope_dim / 2 > 0 ? rope_dim / 2 : 1));
+    orc_rope_inv_freq(inv, rope_dim, base);
+    for (int b = 0; b < rows; ++b)
+        for (int h = 0; h < n_heads; ++h) {
+            float* v = buf + (size_t)b * row_stride + (size_t)h * D;
+            orc_rmsnorm(v, v, gamma, D, eps);
+            orc_rope(v, pos0 + b, rope_dim, inv);
+        }
+    free(inv);
+}
+
+/* ------------------------------------------------------------------ KV append
+ * src/model.cpp:186-189 (per token) and src/cuda/model_cuda.cu:108-117 (per chunk):
+ * cache row (pos0+b) of width kd receives the K (and V) slice of input row b. */
+ORC_API void orc_kv_append(const float* k_src, const float* v_src, long src_stride, int rows, float* kc, float* vc,
+                           int kd, int pos0) {
+    for (int b = 0; b < rows; ++b) {
+        memcpy(kc + (size_t)(pos0 + b) * kd, k_src + (size_t)b * src_stride, sizeof(float) * (size_t)kd);
+        memcpy(vc + (size_t)(pos0 + b) * kd, v_src + (size_t)b * src_stride, sizeof(float) * (size_t)kd);
+    }
+}
+
+/* ------------------------------------------------------------------ attention, one query row
+ * src/model.cpp:191-214.  For each query head hd (OpenMP over heads):
+ *   kvh = hd / group;  s_t = (sum_i q_i k_{t,i}) * scale  (sequential float);  mx = running max;
+ *   e_t = exp(s_t - mx) (float);  sum = sum double(e_t);  inv = float(1/sum);
+ *   out_i = sum_t (e_t * inv) * v_{t,i}, accumulated sequentially in t.
+ * Cache layout [pos][HKV][D]; T = number of visible keys (pos+1).
+ * `scores` is caller scratch of H*T floats (NULL -> allocated here). */
+static void orc_attn_head(const float* q, const float* kc, const float* vc, float* out, int T, int kvh, int HKV,
+                          int D, float scale, float* sc) {
+    const size_t KD = (size_t)HKV * D;
+    float mx = -INFINITY;
+    for (int t = 0; t < T; ++t) {
+        const float* k = kc + (size_t)t * KD + (size_t)kvh * D;
+        float s = 0.f;
+        for (int i = 0; i < D; ++i) s += q[i] * k[i];
+        sc[t] = s * scale;
+        if (sc[t] > mx) mx = sc[t];
+    }
+    double sum = 0.0;
+    for (int t = 0; t < T; ++t) {
+        sc[t] = expf(sc[t] - mx);
+        sum += sc[t];
+    }
+    const float inv = (float)(1.0 / sum);
+    for (int i = 0; i < D; ++i) out[i] = 0.f;
+    for (int t = 0; t < T; ++t) {
+        const float* v = vc + (size_t)t * KD + (size_t)kvh * D;
+        const float p = sc[t] * inv;
+        for (int i = 0; i < D; ++i) out[i] += p * v[i];
+    }
+}
+
+ORC_API void orc_attn_decode(const float* q, const float* kc, const float* vc, float* out, int T, int H, int HKV,
+                             int D, float scale, float* scores) {
+    const int group = H / HKV;
+    float* sc = scores ? scores : (float*)malloc(sizeof(float) * (size_t)H * (size_t)(T > 0 ? T : 1));
+#pragma omp parallel for schedule(static)
+    for (int hd = 0; hd < H; ++hd)
+        orc_attn_head(q + (size_t)hd * D, kc, vc, out + (size_t)hd * D, T, hd / group, HKV, D, scale,
+                      sc + (size_t)hd * T);
+    if (!scores) free(sc);
+}
+
+/* Causal prefill as the reference CPU backend runs it: one token at a time
+ * (src/model.cpp:138-140), query b at position pos0+b seeing keys 0..pos0+b.
+ * q row b at q + b*q_stride; out row b at out + b*H*D. */
+ORC_API void orc_attn_prefill(const float* q, long q_stride, const float* kc, const float* vc, float* out, int B,
+                              int pos0, int H, int HKV, int D, float scale) {
+    const int Tmax = pos0 + B;
+    float* sc = (float*)malloc(sizeof(float) * (size_t)H * (size_t)(Tmax > 0 ? Tmax : 1));
+    for (int b = 0; b < B; ++b)
+        orc_attn_decode(q + (size_t)b * q_stride, kc, vc, out + (size_t)b * H * D, pos0 + b + 1, H, HKV, D, scale,
+                        sc);
+    free(sc);
+}
+
+/* Ragged multi-sequence decode: sequence s has its own cache rows starting at kv_offset[s]
+ * (row = HKV*D floats) and kv_len[s] visible keys; each sequence is one orc_attn_decode. */
+ORC_API void orc_attn_decode_batched(const float* q, const float* kc, const float* vc, float* out,
+                                     const int64_t* kv_offset, const int* kv_len, int nseq, int H, int HKV, int D,
+                                     float scale) {
+    const size_t KD = (size_t)HKV * D;
+    for (int s = 0; s < nseq; ++s)
+        orc_attn_decode(q + (size_t)s * H * D, kc + (size_t)kv_offset[s] * KD, vc + (size_t)kv_offset[s] * KD,
+                        out + (size_t)s * H * D, kv_len[s], H, HKV, D, scale, NULL);
+}
+
+/* ------------------------------------------------------------------ split-K restatement
+ * src/cuda/model_cuda.cu:1043-1111 (k_attn_split + k_attn_combine): the T keys are cut into
+ * nsplit chunks of ceil(T/nsplit); per chunk, 32-key tiles with a running (m, l, acc) and
+ * expf; the combine takes M = max m_s, skips empty chunks (m = -inf) and returns
+ * sum exp(m_s-M) acc_s / sum exp(m_s-M) l_s.  Scores use a plain sequential dot here (the
+ * reference's lane-strided warp sum only changes rounding). */
+ORC_API void orc_attn_split_combine(const float* q, const float* kc, const float* vc, float* out, int T, int H,
+                                    int HKV, int D, float scale, int nsplit) {
+    const int group = H / HKV;
+    const size_t KD = (size_t)HKV * D;
+    const int chunk = (T + nsplit - 1) / nsplit;
+    float* pacc = (float*)malloc(sizeof(float) * (size_t)nsplit * D);
+    float* pm = (float*)malloc(sizeof(float) * (size_t)nsplit);
+    float* pl = (float*)malloc(sizeof(float) * (size_t)nsplit);
+    float sc[32];
+    for (int h = 0; h < H; ++h) {
+        const float* qh = q + (size_t)h * D;
+        const int kvh = h / group;
+        for (int s = 0; s < nsplit; ++s) {
+            const int tb = s * chunk, te = tb + chunk < T ? tb + chunk : T;
+            float m = -INFINITY, l = 0.f;
+            float* acc = pacc + (size_t)s * D;
+            for (int i = 0; i < D; ++i) acc[i] = 0.f;
+            for (int t0 = tb; t0 < te; t0 += 32) {
+                float tm = -INFINITY;
+                for (int j = 0; j < 32; ++j) {
+                    const int t = t0 + j;
+                    float sv = -INFINITY;
+                    if (t < te) {
+                        const float* k = kc + (size_t)t * KD + (size_t)kvh * D;
+                        float p = 0.f;
+                        for (int i = 0; i < D; ++i) p += qh[i] * k[i];
+                        sv = p * scale;
+                    }
+                    sc[j] = sv;
+                    tm = sv > tm ? sv : tm;
+                }
+                const float mn = m > tm ? m : tm;
+                const float corr = expf(m - mn);
+                l *= corr;
+                for (int i = 0; i < D; ++i) acc[i] *= corr;
+                const int lim = te - t0 < 32 ? te - t0 : 32;
+                for (int j = 0; j < lim; ++j) {
+                    const float p = expf(sc[j] - mn);
+                    l += p;
+                    const float* v = vc + (size_t)(t0 + j) * KD + (size_t)kvh * D;
+                    for (int i = 0; i < D; ++i) acc[i] += p * v[i];
+                }
+                m = mn;
+            }
+            pm[s] = m;
+            pl[s] = l;
+        }
+        float M = -INFINITY;
+        for (int s = 0; s < nsplit; ++s) M = pm[s] > M ? pm[s] : M;
+        for (int i = 0; i < D; ++i) {
+            float lsum = 0.f, o = 0.f;
+            for (int s = 0; s < nsplit; ++s) {
+                if (pm[s] == -INFINITY) continue;
+                const float w = expf(pm[s] - M);
+                lsum += w * pl[s];
+                o += w * pacc[(size_t)s * D + i];
+            }
+            out[(size_t)h * D + i] = o / lsum;
+        }
+    }
+    free(pacc);
+    free(pm);
+    free(pl);
+}
+
+/* ------------------------------------------------------------------ float64 brute force
+ * Textbook softmax attention for one query row with T visible keys, everything in double:
+ * out_h = sum_t softmax_t(q_h . k_t * scale) v_t, GQA kvh = h / (H/HKV).  Used to measure
+ * the fp32 paths' distance from exact arithmetic.  Writes double outputs. */
+ORC_API void orc_attn_f64(const float* q, const float* kc, const float* vc, double* out, int T, int H, int HKV,
+                          int D, double scale) {
+    const int group = H / HKV;
+    const size_t KD = (size_t)HKV * D;
+    double* s = (double*)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+    for (int h = 0; h < H; ++h) {
+        const int kvh = h / group;
+        double mx = -INFINITY;
+        for (int t = 0; t < T; ++t) {
+            double a = 0.0;
+            for (int i = 0; i < D; ++i) a += (double)q[(size_t)h * D + i] * kc[(size_t)t * KD + (size_t)kvh * D + i];
+            s[t] = a * scale;
+            if (s[t] > mx) mx = s[t];
+        }
+        double sum = 0.0;
+        for (int t = 0; t < T; ++t) {
+            s[t] = exp(s[t] - mx);
+            sum += s[t];
+        }
+        for (int i = 0; i < D; ++i) {
+            double o = 0.0;
+            for (int t = 0; t < T; ++t) o += s[t] * vc[(size_t)t * KD + (size_t)kvh * D + i];
+            out[(size_t)h * D + i] = o / sum;
+        }
+    }
+    free(s);
+}
+
+ORC_API int orc_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+ORC_API void orc_set_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}

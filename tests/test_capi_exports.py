@@ -1,0 +1,66 @@
+"""The C-ABI library loads and exports every symbol include/ei_attn.h declares (CPU only:
+no compute call needs a GPU here; host-only entry points and argument checks are run)."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from tests.parity import bits_equal
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _declared():
+    text = (ROOT / "include" / "ei_attn.h").read_text()
+    return sorted(set(re.findall(r"\b(ei_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    from exactinfer_amd import _capi
+    assert sorted(_capi.EXPORTS) == _declared()
+
+
+def test_library_exports_every_declared_symbol():
+    from exactinfer_amd import _capi
+    L = _capi.lib()
+    for name in _declared():
+        assert isinstance(getattr(L, name), ctypes._CFuncPtr), name
+    assert L.ei_abi_version() == 1
+
+
+def test_rope_table_fill_host_matches_oracle(orc):
+    from exactinfer_amd import _capi
+    for n_ctx, rd, th in ((64, 128, 1e6), (10, 64, 1e4)):
+        out = np.empty((n_ctx, rd // 2, 2), np.float32)
+        _capi.call("ei_rope_table_fill", out.ctypes.data, n_ctx, rd, th)
+        assert bits_equal(out, orc.rope_table(n_ctx, rd, th))
+
+
+def test_argument_errors_are_reported_not_thrown():
+    from exactinfer_amd import _capi
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    with pytest.raises(_capi.EiError, match="head_dim 64"):
+        _capi.call("ei_attn_prefill", None, p, 4096, p, p, p, p, 8, 32, 8, 64, 0.1)
+    with pytest.raises(_capi.EiError, match="GQA group 3"):
+        _capi.call("ei_attn_prefill", None, p, 4096, p, p, p, p, 8, 24, 8, 128, 0.1)
+    with pytest.raises(_capi.EiError, match="multiple of n_head_kv"):
+        _capi.call("ei_attn_decode", None, p, p, p, p, p, 30, 8, 128, 0.1, 10, p, 1 << 20)
+    with pytest.raises(_capi.EiError, match="workspace"):
+        _capi.call("ei_attn_decode", None, p, p, p, p, p, 32, 8, 128, 0.1, 4096, p, 16)
+    with pytest.raises(_capi.EiError, match="aligned"):
+        _capi.call("ei_kv_append", None, ctypes.c_void_p(18), p, 1024, 1, p, p, 1024, p)
+    with pytest.raises(_capi.EiError, match="rope_dim"):
+        _capi.call("ei_headnorm_rope", None, p, 1, 4096, 32, 128, p, p, p, 130, 1e-6)
+    assert "rope_dim" in _capi.last_error()
+
+
+def test_decode_workspace_size_is_monotone():
+    from exactinfer_amd import _capi
+    L = _capi.lib()
+    a = L.ei_attn_decode_ws_bytes(1, 32, 8, 4096)
+    b = L.ei_attn_decode_ws_bytes(1, 32, 8, 32768)
+    c = L.ei_attn_decode_ws_bytes(64, 16, 8, 8192)
+    assert 0 < a <= b and c > 0
+    assert L.ei_attn_decode_ws_bytes(1, 30, 8, 10) == 0

@@ -1,0 +1,237 @@
+"""Pins of the CPU oracle (CPU only).
+
+Each oracle function is checked by something other than a retyping of its own formula:
+the reference's own functions compiled from source (oracle/_ref), float64 brute force,
+closed forms and invariants chosen so that a dropped term, a swapped operand or a wrong
+index fails at least one of them.
+"""
+import numpy as np
+import pytest
+
+from tests.parity import ATTN_RTOL, bits_equal, rel_err
+
+D = 128
+
+
+# ---------------------------------------------------------------- generator
+def test_generator_moments_and_determinism(orc):
+    x = orc.normal((200000,), 42)
+    assert abs(float(x.mean())) < 0.01 and abs(float(x.std()) - 1.0) < 0.01
+    assert np.abs(x).max() <= 6.0
+    assert bits_equal(orc.normal((1000,), 42, 500), x[500:1500])  # counter-based: offsets compose
+    assert not bits_equal(orc.normal((1000,), 43), x[:1000])
+
+
+# ---------------------------------------------------------------- QK-norm (src/ops.cpp:155-160)
+def test_rmsnorm_bit_exact_vs_reference_source(orc):
+    R = orc.ref_lib()
+    if R is None:
+        pytest.skip("reference tree absent: oracle/_ref not built")
+    for s in range(200):
+        scale = np.float32(10.0 ** ((s % 9) - 4))
+        x = orc.normal((D,), 1000 + s) * scale
+        w = orc.gamma(D, 2000 + s)
+        ref = np.empty_like(x)
+        R.elref_rmsnorm(ref, np.ascontiguousarray(x), w, D, 1e-6)
+        assert bits_equal(orc.rmsnorm(x, w), ref)
+
+
+def test_rmsnorm_closed_forms(orc):
+    # constant vector c: rms = |c| (up to eps) -> out = sign(c) * w
+    w = orc.gamma(D, 5)
+    out = orc.rmsnorm(np.full(D, 3.0, np.float32), w, eps=0.0)
+    assert np.allclose(out, w, rtol=1e-6)
+    # float64 restatement of the definition on random input
+    x = orc.normal((D,), 6) * np.float32(7)
+    x64 = x.astype(np.float64)
+    exact = x64 / np.sqrt(np.mean(x64 * x64) + 1e-6) * w.astype(np.float64)
+    assert np.max(np.abs(orc.rmsnorm(x, w) - exact) / np.abs(exact).max()) < 5e-7
+    # eps matters: a tiny vector is not blown up to unit rms
+    tiny = np.full(D, 1e-5, np.float32)
+    assert np.all(np.abs(orc.rmsnorm(tiny, np.ones(D, np.float32))) < 0.02)
+
+
+# ---------------------------------------------------------------- RoPE (src/model.cpp:23-32, :105-109)
+def test_rope_bit_exact_vs_reference_source(orc):
+    R = orc.ref_lib()
+    if R is None:
+        pytest.skip("reference tree absent: oracle/_ref not built")
+    for rope_dim, base in ((128, 1e6), (64, 1e4), (128, 1e4)):
+        f = orc.rope_inv_freq(rope_dim, base)
+        f_ref = np.empty(rope_dim // 2)
+        R.elref_rope_inv_freq(f_ref, rope_dim, base)
+        assert np.array_equal(f, f_ref)
+        for pos in (0, 1, 7, 511, 4095, 32767, 131071):
+            v = orc.normal((rope_dim,), pos + 3)
+            r = v.copy()
+            R.elref_rope(r, pos, rope_dim, f_ref)
+            assert bits_equal(orc.rope(v, pos, f), r)
+
+
+def test_rope_invariants(orc):
+    f = orc.rope_inv_freq(128, 1e6)
+    v = orc.normal((128,), 9)
+    assert bits_equal(orc.rope(v, 0, f), v)  # position 0 is the identity
+    for pos in (1, 100, 30000):
+        r = orc.rope(v, pos, f).astype(np.float64)
+        # each (i, i+64) pair is rotated: its norm is preserved
+        n0 = v[:64].astype(np.float64) ** 2 + v[64:].astype(np.float64) ** 2
+        n1 = r[:64] ** 2 + r[64:] ** 2
+        assert np.allclose(n0, n1, rtol=1e-6)
+        # pair 0 rotates by exactly pos radians (inv_freq[0] = 1)
+        ang = np.arctan2(r[64], r[0]) - np.arctan2(v[64], v[0])
+        assert abs(np.angle(np.exp(1j * (ang - pos)))) < 1e-5
+    # relative-position property of q.k after rotation (the reason RoPE exists)
+    q, k = orc.normal((128,), 10), orc.normal((128,), 11)
+    d1 = np.dot(orc.rope(q, 50, f).astype(np.float64), orc.rope(k, 40, f).astype(np.float64))
+    d2 = np.dot(orc.rope(q, 1010, f).astype(np.float64), orc.rope(k, 1000, f).astype(np.float64))
+    assert abs(d1 - d2) < 1e-4 * np.linalg.norm(q) * np.linalg.norm(k)
+
+
+def test_rope_table_equals_rope_of_unit_vectors(orc):
+    """cs[p][i] is what rope() applies: rotating e_i gives (cos, sin) at (i, i+half)."""
+    n_ctx = 50
+    cs = orc.rope_table(n_ctx, 128, 1e6)
+    f = orc.rope_inv_freq(128, 1e6)
+    for p in (0, 1, 17, 49):
+        for i in (0, 5, 63):
+            e = np.zeros(128, np.float32)
+            e[i] = 1.0
+            r = orc.rope(e, p, f)
+            assert r[i] == cs[p, i, 0] and r[i + 64] == cs[p, i, 1]
+
+
+def test_headnorm_rope_rows_and_heads(orc):
+    """Row b uses position pos0+b; heads are independent; columns past the heads untouched."""
+    H, rows, pos0 = 3, 4, 10
+    buf = orc.normal((rows, H * D + 8), 12)
+    g = orc.gamma(D, 13)
+    out = orc.headnorm_rope(buf, H, D, g, pos0, 128, 1e6, 1e-6)
+    f = orc.rope_inv_freq(128, 1e6)
+    for b in range(rows):
+        for h in range(H):
+            exp = orc.rope(orc.rmsnorm(buf[b, h * D:(h + 1) * D], g), pos0 + b, f)
+            assert bits_equal(out[b, h * D:(h + 1) * D], exp)
+        assert bits_equal(out[b, H * D:], buf[b, H * D:])
+
+
+# ---------------------------------------------------------------- KV append (src/model.cpp:186-189)
+def test_kv_append_writes_only_target_rows(orc):
+    kd, n_ctx = 1024, 32
+    kc = np.full((n_ctx, kd), 1.5, np.float32)
+    vc = np.full((n_ctx, kd), -2.5, np.float32)
+    k = orc.normal((3, kd), 1)
+    v = orc.normal((3, kd), 2)
+    orc.kv_append(k, v, kc, vc, 20)
+    assert bits_equal(kc[20:23], k) and bits_equal(vc[20:23], v)
+    assert np.all(kc[:20] == 1.5) and np.all(kc[23:] == 1.5)
+    assert np.all(vc[:20] == -2.5) and np.all(vc[23:] == -2.5)
+
+
+# ---------------------------------------------------------------- attention (src/model.cpp:191-214)
+def _kv(orc, T, HKV, seed):
+    return orc.normal((T, HKV, D), seed), orc.normal((T, HKV, D), seed + 1)
+
+
+@pytest.mark.parametrize("H,HKV,T", [(4, 2, 1), (8, 2, 17), (16, 8, 300), (32, 8, 1000)])
+def test_attn_decode_vs_float64(orc, H, HKV, T):
+    k, v = _kv(orc, T, HKV, T)
+    q = orc.normal((H, D), T + 100)
+    out = orc.attn_decode(q, k, v, T, H, HKV, D)
+    exact = orc.attn_f64(q, k, v, T, H, HKV, D)
+    assert rel_err(out, exact) <= ATTN_RTOL
+
+
+def test_attn_f64_textbook(orc):
+    """Independent numpy float64 softmax attention (GQA by np.repeat, as the reference's
+    numpy reference does, tests/parity_reference.py:77-82)."""
+    H, HKV, T = 8, 2, 40
+    k, v = _kv(orc, T, HKV, 3)
+    q = orc.normal((H, D), 4)
+    kk = np.repeat(k.astype(np.float64), H // HKV, axis=1)
+    vv = np.repeat(v.astype(np.float64), H // HKV, axis=1)
+    scale = np.float64(np.float32(1.0) / np.sqrt(np.float32(D)))  # the float scale, used in double
+    s = np.einsum("hd,thd->ht", q.astype(np.float64), kk) * scale
+    s = np.exp(s - s.max(axis=1, keepdims=True))
+    s /= s.sum(axis=1, keepdims=True)
+    exp = np.einsum("ht,thd->hd", s, vv)
+    got = orc.attn_f64(q, k, v, T, H, HKV, D)
+    assert np.max(np.abs(got - exp)) < 1e-12
+
+
+def test_attn_closed_forms(orc):
+    H, HKV = 8, 4
+    # one key: the output is that key's V row exactly (p = 1)
+    k, v = _kv(orc, 1, HKV, 7)
+    q = orc.normal((H, D), 8)
+    out = orc.attn_decode(q, k, v, 1, H, HKV, D)
+    for h in range(H):
+        assert bits_equal(out[h], v[0, h // (H // HKV)])
+    # identical keys: uniform softmax -> mean of V
+    T = 64
+    k = np.repeat(orc.normal((1, HKV, D), 9), T, axis=0)
+    v = orc.normal((T, HKV, D), 10)
+    out = orc.attn_decode(q, k, v, T, H, HKV, D)
+    for h in range(H):
+        assert np.allclose(out[h], v[:, h // (H // HKV)].astype(np.float64).mean(0), rtol=1e-5, atol=1e-6)
+    # a dominant score selects its V row
+    T = 50
+    k, v = _kv(orc, T, HKV, 11)
+    qd = np.zeros((H, D), np.float32)
+    qd[:, 0] = 400.0
+    k[:, :, 0] = 0.0
+    k[23, :, 0] = 1.0
+    out = orc.attn_decode(qd, k, v, T, H, HKV, D)
+    for h in range(H):
+        assert np.allclose(out[h], v[23, h // (H // HKV)], rtol=1e-5, atol=1e-6)
+
+
+def test_attn_gqa_equals_repeated_kv(orc):
+    H, HKV, T = 16, 4, 90
+    k, v = _kv(orc, T, HKV, 20)
+    q = orc.normal((H, D), 21)
+    gqa = orc.attn_decode(q, k, v, T, H, HKV, D)
+    kr = np.ascontiguousarray(np.repeat(k, H // HKV, axis=1))
+    vr = np.ascontiguousarray(np.repeat(v, H // HKV, axis=1))
+    mha = orc.attn_decode(q, kr, vr, T, H, H, D)
+    assert bits_equal(gqa, mha)
+
+
+def test_prefill_is_per_token_decode_and_causal(orc):
+    H, HKV, B, pos0 = 8, 2, 20, 5
+    k, v = _kv(orc, pos0 + B, HKV, 30)
+    q = orc.normal((B, H * D), 31)
+    out = orc.attn_prefill(q, k, v, B, pos0, H, HKV, D)
+    for b in (0, 7, 19):
+        assert bits_equal(out[b], orc.attn_decode(q[b].reshape(H, D), k, v, pos0 + b + 1, H, HKV, D))
+    # causality: future keys do not change earlier rows
+    k2, v2 = k.copy(), v.copy()
+    k2[pos0 + 10:] = 99.0
+    v2[pos0 + 10:] = -99.0
+    out2 = orc.attn_prefill(q, k2, v2, B, pos0, H, HKV, D)
+    assert bits_equal(out[:10], out2[:10]) and not bits_equal(out[10:], out2[10:])
+
+
+def test_split_combine_equals_single_pass(orc):
+    H, HKV, T = 8, 4, 2000
+    k, v = _kv(orc, T, HKV, 50)
+    k[::512] *= np.float32(4.0)
+    q = orc.normal((H, D), 51)
+    single = orc.attn_decode(q, k, v, T, H, HKV, D)
+    exact = orc.attn_f64(q, k, v, T, H, HKV, D)
+    for ns in (1, 16, 37, 2000, 2500):  # includes empty splits (ns > T)
+        sc = orc.attn_split_combine(q, k, v, T, H, HKV, D, nsplit=ns)
+        assert rel_err(sc, single) <= ATTN_RTOL
+        assert rel_err(sc, exact) <= ATTN_RTOL
+
+
+def test_batched_equals_per_sequence(orc):
+    H, HKV = 8, 4
+    lens = np.array([1, 5, 300, 64], np.int32)
+    offs = np.array([0, 10, 20, 400], np.int64)
+    k, v = _kv(orc, 500, HKV, 60)
+    q = orc.normal((4, H * D), 61)
+    out = orc.attn_decode_batched(q, k, v, offs, lens, H, HKV, D)
+    for s in range(4):
+        ref = orc.attn_decode(q[s].reshape(H, D), k[offs[s]:], v[offs[s]:], int(lens[s]), H, HKV, D)
+        assert bits_equal(out[s], ref)
