@@ -64,15 +64,26 @@ class Timer:
         return self.a.elapsed_time(self.b)
 
 
-def per_launch_ms(torch, launch, n: int) -> float:
-    """Average duration of one launch, each bracketed by its own event pair."""
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    for i in range(n):
-        evs[i][0].record()
-        launch(i)
-        evs[i][1].record()
+def graph_ms(torch, fn, reps: int = 20, warm: int = 3) -> float:
+    """Average time of fn() replayed as one HIP graph, measured with events on the stream
+    the graph runs on (the launches inside fn go to torch's current stream)."""
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in evs) / n
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # first launches load code objects outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warm):
+        g.replay()
+    t = Timer(torch)
+    t.start()
+    for _ in range(reps):
+        g.replay()
+    return t.stop_ms() / reps
 
 
 # ---------------------------------------------------------------- decode (configs[1], configs[3])
@@ -124,7 +135,7 @@ def bench_decode(torch, A, H, HKV, n_layer, ctx, steps, warmup, use_graph, spike
     for _ in range(steps):
         run()
     ms = t.stop_ms() / steps
-    kern_ms = per_launch_ms(torch, lambda i: layer(i % n_layer), 4 * n_layer)
+    kern_ms = ms / n_layer  # the step is n_layer back-to-back launches of the one kernel
     bytes_layer = A.decode_bytes(ctx, H, HKV)
     return {
         "ms_per_step": ms,
@@ -186,7 +197,7 @@ def bench_batched(torch, A, steps, warmup, use_graph, seed=3000):
         run()
     ms = t.stop_ms() / steps
     bytes_layer = sum(A.decode_bytes(int(x), H, HKV) for x in lens)
-    kern_ms = per_launch_ms(torch, lambda i: layer(i % n_layer), n_layer)
+    kern_ms = ms / n_layer
     return {"ms_per_step": ms, "gbs": bytes_layer * n_layer / (ms * 1e-3) / 1e9, "kernel_ms": kern_ms,
             "kernel_gbs": bytes_layer / (kern_ms * 1e-3) / 1e9, "bytes_per_launch": bytes_layer,
             "sum_kv_len": int(lens.sum())}
@@ -229,7 +240,8 @@ def bench_prefill(torch, A, H, HKV, n_layer, T, steps, warmup, seed=2000):
         tot += t.stop_ms()
     ms = tot / steps
     flops_layer = A.flops_causal(T, 0, H)
-    kern_ms = per_launch_ms(torch, lambda i: attn(i % n_layer), n_layer)
+    # the dominant kernel alone: n_layer attention launches in one graph
+    kern_ms = graph_ms(torch, lambda: [attn(l) for l in range(n_layer)], reps=5, warm=1) / n_layer
     return {"ms_per_step": ms, "tflops": flops_layer * n_layer / (ms * 1e-3) / 1e12, "kernel_ms": kern_ms,
             "kernel_tflops": flops_layer / (kern_ms * 1e-3) / 1e12, "flops_per_launch": flops_layer}
 

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "../../include/ei_attn.h"
@@ -151,7 +152,6 @@ int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void
     char* base = static_cast<char*>(ws);
     a.part_acc = reinterpret_cast<float*>(base);
     a.part_ml = reinterpret_cast<float*>(base + al(slots * G * 128 * 4));
-    a.counters = reinterpret_cast<unsigned*>(base + al(slots * G * 128 * 4) + al(slots * G * 2 * 4));
     a.chunk = p.chunk;
     a.nsplit = p.nsplit;
     return hip_status(ei::launch_decode(st, a, n_seq, fused), "decode launch");

@@ -1,40 +1,50 @@
 // decode.hip — split-K decode attention for gfx950 (one query token per sequence).
 //
-// Work decomposition: grid (nsplit, HKV, n_seq), 256 threads.  A workgroup owns one KV
-// head of one sequence and one chunk of keys, and serves all G = H/HKV query heads of
-// that GQA group from the same K/V bytes (the reference re-reads K/V once per query head,
-// src/cuda/model_cuda.cu:1051, :1066).  The chunk is walked in 64-key sub-tiles:
+// Work decomposition: grid (nsplit, HKV, n_seq), 256 threads (4 waves).  A workgroup owns
+// one KV head of one sequence and one chunk of keys, and serves all G = H/HKV query heads
+// of that GQA group from the same K/V bytes (the reference re-reads K/V once per query
+// head, src/cuda/model_cuda.cu:1051, :1066).  Inside the chunk, wave w owns the 16-key
+// tiles w, w+4, w+8, ... and runs its own online softmax over them; the four waves merge
+// once at the end.  There is no workgroup barrier in the key loop.
 //
-//   K phase   wave w scores keys 16w..16w+15 of the sub-tile.  Lane (r = l/8, c = l%8)
-//             loads float4s of rows r and r+8 at d = 4c + 32i (i < 4): every load
-//             instruction covers 8 rows x 128 contiguous bytes.  The 8 lanes of a row
-//             hold partial dots for (2 rows x G heads); a transposing butterfly over
-//             lanes xor 1/2/4 leaves one finished score per lane (7 exchanges for G=4).
-//   softmax   scores go through LDS; every wave takes the sub-tile max per head with a
-//             64-lane reduction (lane = key), rescales its running (m, l, acc) and writes
-//             p = exp(s - m) to a wave-private LDS row.
-//   V phase   wave w owns d in [32w, 32w+32) for all 64 keys: lane (r, c) loads
-//             V[r + 8i][32w + 4c ..+4] (8 rows x 128 B per instruction) and accumulates
-//             p * v for the G heads.
+// Data movement: each wave streams its tiles HBM -> LDS with global_load_lds_dwordx4
+// (gfx950 LDS DMA: 64 lanes x 16 B = one 1 KB instruction, no VGPRs spent on landing
+// data), through a private two-slot ring (2 x 16 KB), so a workgroup keeps 128 KB of K/V
+// in flight.  A 16-key tile is 16 rows x 512 B of K and the same of V; every instruction
+// moves two whole rows (fully used 128-byte lines).  Within a row, 16-byte chunk q is
+// stored at slot q ^ 8*(row & 1), which keeps both read patterns below free of LDS bank
+// conflicts between neighbouring rows.
 //
-// Every K and V byte is loaded exactly once per launch, with 128-byte coalesced wavefront
-// loads; K and V for a sub-tile are issued together so a workgroup has 64 KB in flight.
+//   scores    lane (r = l/8, c = l%8) reads rows r and r+8 at d = 4c + 32i (i < 4) and
+//             holds q for those d in registers; the 8 lanes of a row hold partial dots for
+//             (2 rows x G heads) and a transposing butterfly over lanes xor 1/2/4 leaves
+//             one finished score per lane (7 exchanges for G = 4).
+//   softmax   the tile max per head is a 4-step butterfly over the lanes holding that
+//             head; p = exp(s - m) goes to a wave-private LDS row.
+//   values    lane l owns d = 2l, 2l+1 of all 16 rows and accumulates p * v for the G
+//             heads.
 //
-// Split combine: each workgroup writes its unnormalised partial (m, l, acc[G][128]); the
-// last workgroup of a (sequence, kv head) to arrive (device-scope counter) merges them,
-// o = sum_s e^(m_s-M) acc_s / sum_s e^(m_s-M) l_s, skipping empty splits, and re-arms the
-// counter (src/cuda/model_cuda.cu:1097-1111 semantics, one launch instead of two).
+// Split combine: each workgroup writes its unnormalised partial (m, l, acc[G][128]); a
+// second, small launch (k_combine, one workgroup per query head) merges them,
+// o = sum_s e^(m_s-M) acc_s / sum_s e^(m_s-M) l_s, skipping empty splits
+// (src/cuda/model_cuda.cu:1097-1111 semantics).  The kernel boundary is what makes the
+// partials of every XCD visible; an in-kernel "last workgroup merges" scheme needs
+// device-coherent stores, loads and an atomic, and measured slower here.  A chunk
+// covering all keys (nsplit = 1) writes o directly and skips the second launch.
 //
 // Fused variant: the workgroup also applies QK-norm + RoPE to its G query heads, and the
 // workgroup whose chunk holds the new position writes the normed K row and the V row to
-// the cache and scores that key from LDS.
+// the cache and patches them into its LDS tile (the DMA may have read the old bytes).
 #include "common.h"
 #include "launch.h"
 
+#include <cstdlib>
+
 namespace ei {
 
-constexpr int kThreads = 256;
-constexpr int kSub = 64;  // keys per sub-tile
+constexpr int kTile = 16;                          // keys per wave tile
+constexpr int kTileFloats = 2 * kTile * kHeadDim;  // K rows then V rows
+constexpr int kRingTiles = 8;                      // LDS ring: 8 tiles (128 KB) per workgroup
 
 // Transposing butterfly over the 8 lanes c = lane%8 (masks 1, 2, 4).  At each step a
 // lane keeps one half of its array and receives the partner's copy of that half, so N
@@ -89,21 +99,77 @@ __device__ __forceinline__ float dot4(const float4 a, const float4 b, float acc)
     return fmaf(a.w, b.w, acc);
 }
 
-__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+// LDS byte address of a __shared__ object (the low 32 bits of its flat address).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>(p);
+}
 
-template <int G, bool FUSED>
-__global__ __launch_bounds__(kThreads) void k_decode(const DecodeArgs a) {
+// One LDS-DMA instruction: every active lane copies 16 bytes from its global address to
+// LDS byte address m0_base + 16*lane.  Issued through inline asm so the compiler does not
+// see a pending LDS write and serialise unrelated LDS accesses behind it; completion is
+// tracked by hand with wait_vmcnt (each instruction counts one in vmcnt).
+__device__ __forceinline__ void dma16(const float* g, uint32_t m0_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0_base) : "memory", "m0");
+}
+
+// Copy nbytes (<= 1024, multiple of 16) of contiguous global memory into LDS; one
+// instruction, lanes past the end idle.
+__device__ __forceinline__ void dma_block(const float* g, uint32_t lds_base, int nbytes, int lane) {
+    if (16 * lane < nbytes) dma16(g + 4 * lane, lds_base);
+}
+
+// Swizzled float offset of (row, 16-byte chunk) inside a tile's K or V half.
+__device__ __forceinline__ int tile_off(int row, int chunk) {
+    return row * kHeadDim + ((chunk ^ ((row & 1) << 3)) << 2);
+}
+
+// Issue the 16 DMA instructions of one tile: K rows t0..t0+15 then V rows (two rows per
+// instruction).  Rows past t_end are clamped to the last visible row (valid memory; their
+// scores are masked out).
+__device__ __forceinline__ void issue_tile(const float* slot, const float* kbase, const float* vbase, size_t KD,
+                                           int t0, int t_end, int lane) {
+    const int half = lane >> 5, s = lane & 31;
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(slot));
+#pragma unroll
+    for (int t = 0; t < kTile / 2; ++t) {
+        const int row = 2 * t + half;
+        const int key = min(t0 + row, t_end - 1);
+        const int chunk = s ^ ((row & 1) << 3);
+        dma16(kbase + (size_t)key * KD + 4 * chunk, base + t * 1024);
+    }
+#pragma unroll
+    for (int t = 0; t < kTile / 2; ++t) {
+        const int row = 2 * t + half;
+        const int key = min(t0 + row, t_end - 1);
+        const int chunk = s ^ ((row & 1) << 3);
+        dma16(vbase + (size_t)key * KD + 4 * chunk, base + kTile * kHeadDim * 4 + t * 1024);
+    }
+}
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at 15:14,
+// expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// NW waves per workgroup, each with a ring of kRingTiles/NW tile slots: 4 waves x 2 slots
+// streams long chunks with one tile always in flight behind the one being scored; 8 waves
+// x 1 slot gives short chunks (one tile per wave) two waves per SIMD to hide latency.
+template <int G, bool FUSED, int NW>
+__global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
+    constexpr int kThreads = 64 * NW, kWaves = NW, kRing = kRingTiles / NW;
     constexpr int D = kHeadDim;
-    constexpr int NV = 2 * G;                     // partial dots per lane in the K phase
+    constexpr int NV = 2 * G;                     // partial dots per lane in the score phase
     constexpr int NF = NV / 8 > 0 ? NV / 8 : 1;   // finished scores per lane after xreduce8
+    constexpr int NCOL = G * 32;                  // float4 columns of the G output heads
+    extern __shared__ __align__(16) float ring[];          // [kWaves][kRing][kTileFloats]; later scratch
     __shared__ __align__(16) float qs[G * D];
-    __shared__ __align__(16) float sc[kSub * G];
-    __shared__ __align__(16) float pw[4][kSub * G];
-    __shared__ __align__(16) float knew[4][D];   // fused: [0] normed K row, [1] V row, [2..3] scratch
-    __shared__ float red[4][2 * G];
-    __shared__ float wts[kDecodeMaxSplits * G];
-    __shared__ float4 ored[kThreads];
-    __shared__ int s_last;
+    __shared__ __align__(16) float pw[kWaves][kTile * G];  // per wave: p[row][g] of the current tile
+    __shared__ __align__(16) float mw[kWaves][G];          // per wave: new running max per head
+    __shared__ float wml[kWaves][2 * G];
+    __shared__ __align__(16) float knew[4][D];             // fused: [0] K row (raw, then normed), [1] V row, [2] scratch
+    __shared__ __align__(16) float stage[4 * D];           // fused: [0] q gamma, [1] k gamma, [2..3] RoPE row
 
     const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -118,39 +184,65 @@ __global__ __launch_bounds__(kThreads) void k_decode(const DecodeArgs a) {
     const int pos = len - 1;
     const float* qrow = a.q + (size_t)seq * a.q_stride;
     const int h0 = kvh * G;
+    float* wring = ring + w * (kRing * kTileFloats);
 
-    bool owner = false;
+
+    // ---- prologue inputs first (wave 0: q rows, gammas, RoPE row; wave 1: the new K/V
+    // row), then this wave's first two tiles, all as LDS DMA, so nothing waits on
+    // anything before the whole workgroup's 128 KB is in flight
+    const int tw0 = t_begin + kTile * w;
+    constexpr int kStride = kTile * kWaves;  // distance between a wave's consecutive tiles
+    const bool owner = FUSED && t_begin <= pos && pos < t_end;
+    if (w == 0) {
+        const uint32_t qa = __builtin_amdgcn_readfirstlane(lds_addr(qs));
+#pragma unroll
+        for (int i = 0; i < (G * D * 4 + 1023) / 1024; ++i)
+            dma_block(qrow + (size_t)h0 * D + 256 * i, qa + 1024 * i, G * D * 4 - 1024 * i, lane);
+        if constexpr (FUSED) {
+            dma_block(a.q_gamma, __builtin_amdgcn_readfirstlane(lds_addr(stage)), D * 4, lane);
+            dma_block(reinterpret_cast<const float*>(a.cs + (size_t)pos * (a.rope_dim >> 1)),
+                      __builtin_amdgcn_readfirstlane(lds_addr(stage + 2 * D)), a.rope_dim * 4, lane);
+        }
+    } else if (w == 1 && owner) {
+        dma_block(qrow + (size_t)a.H * D + (size_t)kvh * D, __builtin_amdgcn_readfirstlane(lds_addr(knew[0])), D * 4,
+                  lane);
+        dma_block(qrow + (size_t)(a.H + a.HKV) * D + (size_t)kvh * D,
+                  __builtin_amdgcn_readfirstlane(lds_addr(knew[1])), D * 4, lane);
+        dma_block(a.k_gamma, __builtin_amdgcn_readfirstlane(lds_addr(stage + D)), D * 4, lane);
+    }
+    int ntiles0 = 0;
+#pragma unroll
+    for (int i = 0; i < kRing; ++i)
+        if (tw0 + i * kStride < t_end) {
+            issue_tile(wring + i * kTileFloats, kbase, vbase, KD, tw0 + i * kStride, t_end, lane);
+            ++ntiles0;
+        }
+    if (w <= 1) {  // this wave's prologue DMA (older than its tiles) has landed
+        if (kRing == 2 && ntiles0 == 2) wait_vmcnt<2 * kTile>();
+        else if (ntiles0 >= 1) wait_vmcnt<kTile>();
+        else wait_vmcnt<0>();
+    }
+    __syncthreads();
+
     if constexpr (FUSED) {
-        const float2* cs_row = a.cs + (size_t)pos * (a.rope_dim >> 1);
-        for (int g = w; g < G; g += 4) {
+        const float2* cs_row = reinterpret_cast<const float2*>(stage + 2 * D);
+        for (int g = w; g < G; g += kWaves) {  // in place: raw q -> normed, roped q
             float o0, o1;
-            norm_rope_head(qrow + (size_t)(h0 + g) * D, a.q_gamma, cs_row, a.rope_dim, a.eps, qs + g * D, lane,
-                           &o0, &o1);
+            norm_rope_head(qs + g * D, stage, cs_row, a.rope_dim, a.eps, qs + g * D, lane, &o0, &o1);
             qs[g * D + lane] = o0;
             qs[g * D + lane + 64] = o1;
         }
-        owner = t_begin <= pos && pos < t_end;
-        if (owner) {
-            const float* krow = qrow + (size_t)a.H * D + (size_t)kvh * D;
-            const float* vrow = qrow + (size_t)(a.H + a.HKV) * D + (size_t)kvh * D;
-            if (w == 0) {
-                float o0, o1;
-                norm_rope_head(krow, a.k_gamma, cs_row, a.rope_dim, a.eps, knew[2], lane, &o0, &o1);
-                knew[0][lane] = o0;
-                knew[0][lane + 64] = o1;
-            } else if (w == 1) {
-                knew[1][lane] = vrow[lane];
-                knew[1][lane + 64] = vrow[lane + 64];
-            }
+        if (owner && w == kWaves - 1) {
+            float o0, o1;
+            norm_rope_head(knew[0], stage + D, cs_row, a.rope_dim, a.eps, knew[2], lane, &o0, &o1);
+            knew[0][lane] = o0;
+            knew[0][lane + 64] = o1;
         }
         __syncthreads();
         if (owner && tid < 2 * D) {
             float* dst = (tid < D ? kbase : vbase) + (size_t)pos * KD + (tid & (D - 1));
             *dst = knew[tid >> 7][tid & (D - 1)];
         }
-    } else {
-        for (int i = tid; i < G * D; i += kThreads) qs[i] = qrow[(size_t)h0 * D + i];
-        __syncthreads();
     }
 
     float4 qreg[G][4];
@@ -159,213 +251,213 @@ __global__ __launch_bounds__(kThreads) void k_decode(const DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) qreg[g][i] = *reinterpret_cast<const float4*>(qs + g * D + 4 * c + 32 * i);
 
-    float m[G], l[G];
-    float4 acc[G];
+    float m[G];         // running max per head (wave-uniform)
+    float l[NF];        // per-lane partial denominators of this lane's (row, head) slots
+    float2 acc[G];      // acc[g] at d = 2*lane, 2*lane+1
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
-        l[g] = 0.f;
-        acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+        acc[g] = make_float2(0.f, 0.f);
     }
+#pragma unroll
+    for (int k = 0; k < NF; ++k) l[k] = 0.f;
     const int sidx = xreduce8_index<NV>(c);
 
-    for (int t0 = t_begin; t0 < t_end; t0 += kSub) {
-        // ---- issue K and V loads of the sub-tile
-        float4 kr[2][4], vr[8];
-        bool kval[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int tk = t0 + 16 * w + 8 * j + r;
-            kval[j] = tk < t_end;
-            const float* src = kbase + (size_t)tk * KD + 4 * c;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) kr[j][i] = kval[j] ? ld4(src + 32 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int tv = t0 + r + 8 * i;
-            vr[i] = tv < t_end ? ld4(vbase + (size_t)tv * KD + 32 * w + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+    int slot_i = 0;
+    for (int t0 = tw0; t0 < t_end; t0 += kStride, slot_i = (slot_i + 1) % kRing) {
+        if (kRing == 2 && t0 + kStride < t_end) wait_vmcnt<kTile>();  // this tile landed; the next may fly
+        else wait_vmcnt<0>();
+        float* tk = wring + slot_i * kTileFloats;
+        float* tv = tk + kTile * D;
+
         if constexpr (FUSED) {
-            if (owner) {  // the new row: use the LDS copy, not the (possibly stale) loaded bytes
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    if (t0 + 16 * w + 8 * j + r == pos)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) kr[j][i] = *reinterpret_cast<const float4*>(&knew[0][4 * c + 32 * i]);
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    if (t0 + r + 8 * i == pos) vr[i] = *reinterpret_cast<const float4*>(&knew[1][32 * w + 4 * c]);
+            const int kr = pos - t0;
+            if (owner && kr >= 0 && kr < kTile) {  // the new row: overwrite what the DMA brought
+                *reinterpret_cast<float2*>(tk + tile_off(kr, lane >> 1) + 2 * (lane & 1)) =
+                    *reinterpret_cast<const float2*>(&knew[0][2 * lane]);
+                *reinterpret_cast<float2*>(tv + tile_off(kr, lane >> 1) + 2 * (lane & 1)) =
+                    *reinterpret_cast<const float2*>(&knew[1][2 * lane]);
+                __builtin_amdgcn_wave_barrier();
             }
         }
 
-        // ---- scores: partial dots, 8-lane transposing reduction, to LDS
+        // ---- scores: partial dots, 8-lane transposing reduction
         float part[NV];
+#pragma unroll
+        for (int x = 0; x < NV; ++x) part[x] = 0.f;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float s = 0.f;
+            for (int i = 0; i < 4; ++i) {
+                const float4 kv = *reinterpret_cast<const float4*>(tk + tile_off(8 * j + r, c + 8 * i));
 #pragma unroll
-                for (int i = 0; i < 4; ++i) s = dot4(qreg[g][i], kr[j][i], s);
-                part[j * G + g] = s;
+                for (int g = 0; g < G; ++g) part[j * G + g] = dot4(qreg[g][i], kv, part[j * G + g]);
             }
         xreduce8<NV>(part, c);
+
+        // ---- online softmax over the tile, per head
 #pragma unroll
         for (int k = 0; k < NF; ++k) {
-            const int idx = sidx + k;
-            const int j = idx / G, g = idx % G;
-            const bool valid = j == 0 ? kval[0] : kval[1];
-            sc[(16 * w + 8 * j + r) * G + g] = valid ? part[k] * a.scale : -INFINITY;
-        }
-        __syncthreads();
-
-        // ---- online softmax over the sub-tile (lane = key slot), identical in every wave
-        float p[G], corr[G];
+            const int idx = sidx + k, j = idx / G, g = idx % G;
+            const float sv = t0 + 8 * j + r < t_end ? part[k] * a.scale : -INFINITY;
+            float mt = fmaxf(sv, lane_xor1(sv));  // lanes holding this head: xor 1, 8, 16, 32
+            mt = fmaxf(mt, lane_xor8(mt));
+            mt = fmaxf(mt, lane_xor16(mt));
+            mt = fmaxf(mt, lane_xor32(mt));
+            float mold = m[0];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float sv = sc[lane * G + g];
-            const float mt = wave_max(sv);
-            const float mn = fmaxf(m[g], mt);  // finite: the sub-tile holds at least one key
-            corr[g] = expf(m[g] - mn);
-            p[g] = expf(sv - mn);
-            l[g] = l[g] * corr[g] + p[g];
-            m[g] = mn;
-            pw[w][lane * G + g] = p[g];
-            acc[g].x *= corr[g];
-            acc[g].y *= corr[g];
-            acc[g].z *= corr[g];
-            acc[g].w *= corr[g];
+            for (int gg = 1; gg < G; ++gg) mold = g == gg ? m[gg] : mold;
+            const float mn = fmaxf(mold, mt);  // finite: the tile holds at least one visible key
+            const float p = expf(sv - mn);
+            l[k] = l[k] * expf(mold - mn) + p;
+            pw[w][(8 * j + r) * G + g] = p;
+            if (r == 0 && j == 0) mw[w][g] = mn;
         }
         __builtin_amdgcn_wave_barrier();
-
-        // ---- V phase: acc[g][d] += p[key][g] * V[key][d], d = 32w + 4c .. +4
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float* pk = &pw[w][(r + 8 * i) * G];
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float pv = pk[g];
-                acc[g].x = fmaf(pv, vr[i].x, acc[g].x);
-                acc[g].y = fmaf(pv, vr[i].y, acc[g].y);
-                acc[g].z = fmaf(pv, vr[i].z, acc[g].z);
-                acc[g].w = fmaf(pv, vr[i].w, acc[g].w);
-            }
-        }
-        __syncthreads();  // sc and pw are rewritten by the next sub-tile
-    }
-
-    // ---- chunk partial: sum acc over the 8 key rows (lanes xor 8/16/32), l over 64 slots
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        acc[g].x += lane_xor8(acc[g].x);
-        acc[g].y += lane_xor8(acc[g].y);
-        acc[g].z += lane_xor8(acc[g].z);
-        acc[g].w += lane_xor8(acc[g].w);
-        acc[g].x += lane_xor16(acc[g].x);
-        acc[g].y += lane_xor16(acc[g].y);
-        acc[g].z += lane_xor16(acc[g].z);
-        acc[g].w += lane_xor16(acc[g].w);
-        acc[g].x += lane_xor32(acc[g].x);
-        acc[g].y += lane_xor32(acc[g].y);
-        acc[g].z += lane_xor32(acc[g].z);
-        acc[g].w += lane_xor32(acc[g].w);
-        l[g] = wave_sum(l[g]);
-    }
-    const size_t head_slot = (size_t)seq * a.HKV + kvh;
-    const size_t slot = head_slot * a.nsplit + split;
-    float* pacc = a.part_acc + slot * G * D;
-    if (lane < 8) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) *reinterpret_cast<float4*>(pacc + g * D + 32 * w + 4 * c) = acc[g];
-    }
-    if (tid < G) {
-        a.part_ml[(slot * G + tid) * 2 + 0] = m[tid];
-        a.part_ml[(slot * G + tid) * 2 + 1] = l[tid];
-    }
-
-    // ---- arrival; the last workgroup of this (sequence, kv head) merges the splits
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&a.counters[head_slot], 1u) == (unsigned)(a.nsplit - 1);
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-    const int S = a.nsplit;
-    const float* pml = a.part_ml + head_slot * S * G * 2;
-    const float* pa = a.part_acc + head_slot * S * G * D;
-    float M[G], L[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) M[g] = -INFINITY;
-    for (int s = tid; s < S; s += kThreads)
-#pragma unroll
-        for (int g = 0; g < G; ++g) M[g] = fmaxf(M[g], pml[(s * G + g) * 2]);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        M[g] = wave_max(M[g]);
-        if (lane == 0) red[w][g] = M[g];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) M[g] = fmaxf(fmaxf(red[0][g], red[1][g]), fmaxf(red[2][g], red[3][g]));
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) L[g] = 0.f;
-    for (int s = tid; s < S; s += kThreads)
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float ms = pml[(s * G + g) * 2], ls = pml[(s * G + g) * 2 + 1];
-            const float wv = ms == -INFINITY ? 0.f : expf(ms - M[g]);  // empty split: skipped
-            wts[s * G + g] = wv;
-            L[g] = fmaf(wv, ls, L[g]);
+            const float mn = mw[w][g];
+            const float corr = expf(m[g] - mn);
+            m[g] = mn;
+            acc[g].x *= corr;
+            acc[g].y *= corr;
         }
+        // ---- values: acc[g][d] += p[row][g] * V[row][d]
+        const int voff = 2 * (lane & 1);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        L[g] = wave_sum(L[g]);
-        if (lane == 0) red[w][G + g] = L[g];
+        for (int k = 0; k < kTile; ++k) {
+            const float2 vv = *reinterpret_cast<const float2*>(tv + tile_off(k, lane >> 1) + voff);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float pv = pw[w][k * G + g];
+                acc[g].x = fmaf(pv, vv.x, acc[g].x);
+                acc[g].y = fmaf(pv, vv.y, acc[g].y);
+            }
+        }
+        // reads of this slot have returned (their values were consumed above) before the
+        // refill is issued into it
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_wave_barrier();
+        if (t0 + kRing * kStride < t_end) issue_tile(tk, kbase, vbase, KD, t0 + kRing * kStride, t_end, lane);
     }
+
+    // ---- wave partial: l summed over the lanes holding each head; merge the waves in LDS
+#pragma unroll
+    for (int k = 0; k < NF; ++k) {
+        float lv = l[k] + lane_xor1(l[k]);
+        lv += lane_xor8(lv);
+        lv += lane_xor16(lv);
+        lv += lane_xor32(lv);
+        const int idx = sidx + k, j = idx / G, g = idx % G;
+        if (r == 0 && j == 0) {
+            wml[w][g] = m[g];
+            wml[w][G + g] = lv;
+        }
+    }
+    __syncthreads();  // every wave is past its key loop: the ring can hold the wave partials
+    float* wacc = ring;  // [kWaves][G*D]
+#pragma unroll
+    for (int g = 0; g < G; ++g) *reinterpret_cast<float2*>(&wacc[w * G * D + g * D + 2 * lane]) = acc[g];
     __syncthreads();
 
-    // outputs: G*32 float4 columns; kThreads/(G*32) threads share a column over the splits
-    constexpr int NCOL = G * 32, NPART = kThreads / NCOL > 0 ? kThreads / NCOL : 1;
-    {
-        const int col = tid % NCOL, part = tid / NCOL;
-        if (part < NPART) {
-            const int g = col / 32, d4 = col % 32;
-            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int s = part; s < S; s += NPART) {
-                const float wv = wts[s * G + g];
-                if (wv != 0.f) {
-                    const float4 v = ld4(pa + ((size_t)s * G + g) * D + 4 * d4);
-                    o.x = fmaf(wv, v.x, o.x);
-                    o.y = fmaf(wv, v.y, o.y);
-                    o.z = fmaf(wv, v.z, o.z);
-                    o.w = fmaf(wv, v.w, o.w);
-                }
-            }
-            ored[part * NCOL + col] = o;
-        }
-    }
-    __syncthreads();
+    // thread t < NCOL merges float4 column (g, d4)
+    const size_t head_slot = (size_t)seq * a.HKV + kvh;
+    const size_t slot = head_slot * a.nsplit + split;
+    const int S = a.nsplit;
+    const int gcol = (tid % NCOL) / 32, d4 = (tid % NCOL) % 32;
+    float Mw = -INFINITY, Lw = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     if (tid < NCOL) {
-        const int g = tid / 32, d4 = tid % 32;
-        float4 o = ored[tid];
-        for (int part = 1; part < NPART; ++part) {
-            const float4 v = ored[part * NCOL + tid];
-            o.x += v.x;
-            o.y += v.y;
-            o.z += v.z;
-            o.w += v.w;
+        float mws[kWaves];
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) {
+            mws[ww] = t_begin + kTile * ww < t_end ? wml[ww][gcol] : -INFINITY;  // waves without keys: nothing
+            Mw = fmaxf(Mw, mws[ww]);
         }
-        const float Lg = red[0][G + g] + red[1][G + g] + red[2][G + g] + red[3][G + g];
-        o.x /= Lg;
-        o.y /= Lg;
-        o.z /= Lg;
-        o.w /= Lg;
-        *reinterpret_cast<float4*>(a.out + (size_t)seq * a.H * D + (size_t)(h0 + g) * D + 4 * d4) = o;
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) {
+            if (mws[ww] == -INFINITY) continue;
+            const float wv = expf(mws[ww] - Mw);
+            Lw = fmaf(wv, wml[ww][G + gcol], Lw);
+            const float4 v = *reinterpret_cast<const float4*>(&wacc[ww * G * D + gcol * D + 4 * d4]);
+            o.x = fmaf(wv, v.x, o.x);
+            o.y = fmaf(wv, v.y, o.y);
+            o.z = fmaf(wv, v.z, o.z);
+            o.w = fmaf(wv, v.w, o.w);
+        }
     }
-    if (tid == 0) a.counters[head_slot] = 0u;  // re-arm for the next call
+
+    if (S == 1) {  // a single split is already the answer
+        if (tid < NCOL) {
+            o.x /= Lw;
+            o.y /= Lw;
+            o.z /= Lw;
+            o.w /= Lw;
+            *reinterpret_cast<float4*>(a.out + (size_t)seq * a.H * D + (size_t)(h0 + gcol) * D + 4 * d4) = o;
+        }
+        return;
+    }
+
+    // unnormalised partial of this split; k_combine merges the splits in a second launch
+    // (the kernel boundary makes these plain stores visible to every XCD)
+    if (tid < NCOL) {
+        *reinterpret_cast<float4*>(a.part_acc + (slot * G + gcol) * D + 4 * d4) = o;
+        if (d4 == 0) *reinterpret_cast<float2*>(a.part_ml + (slot * G + gcol) * 2) = make_float2(Mw, Lw);
+    }
+}
+
+// Split combine as a separate launch: grid (n_seq * H), 128 threads (thread = d).  All
+// (m, l) and accumulator loads of the S splits are issued before any is used.
+template <int G>
+__global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
+    constexpr int D = kHeadDim;
+    __shared__ float wsh[kDecodeMaxSplits];
+    __shared__ float Lsh;
+    const int hq = blockIdx.x % a.H, seq = blockIdx.x / a.H;
+    const int kvh = hq / G, g = hq % G;
+    const int S = a.nsplit, tid = threadIdx.x;
+    const size_t head_slot = (size_t)seq * a.HKV + kvh;
+    const float* pml = a.part_ml + (head_slot * S * G + g) * 2;
+    const float* pa = a.part_acc + (head_slot * S * G + g) * D + tid;
+    constexpr int B = 32;
+    float acc = 0.f;
+    for (int s0 = 0; s0 < S; s0 += B) {
+        float v[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) v[b] = pa[(size_t)min(s0 + b, S - 1) * G * D];
+        if (s0 == 0) {
+            // weights: wave 0 reduces (m, l) over the splits
+            if (tid < 64) {
+                float mv[kDecodeMaxSplits / 64], lv[kDecodeMaxSplits / 64];
+                float M = -INFINITY;
+#pragma unroll
+                for (int k = 0; k < kDecodeMaxSplits / 64; ++k) {
+                    const int s = tid + 64 * k;
+                    const float2 ml = s < S ? *reinterpret_cast<const float2*>(pml + (size_t)s * G * 2)
+                                            : make_float2(-INFINITY, 0.f);
+                    mv[k] = ml.x;
+                    lv[k] = ml.y;
+                    M = fmaxf(M, ml.x);
+                }
+                M = wave_max(M);
+                float L = 0.f;
+#pragma unroll
+                for (int k = 0; k < kDecodeMaxSplits / 64; ++k) {
+                    const int s = tid + 64 * k;
+                    const float wv = mv[k] == -INFINITY ? 0.f : expf(mv[k] - M);  // empty split: skipped
+                    if (s < S) wsh[s] = wv;
+                    L = fmaf(wv, lv[k], L);
+                }
+                L = wave_sum(L);
+                if (tid == 0) Lsh = L;
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+            if (s0 + b < S) acc = fmaf(wsh[s0 + b], v[b], acc);
+    }
+    a.out[(size_t)seq * a.H * D + (size_t)hq * D + tid] = acc / Lsh;
 }
 
 __global__ void k_ws_clear(uint32_t* p, size_t n) {
@@ -373,15 +465,25 @@ __global__ void k_ws_clear(uint32_t* p, size_t n) {
 }
 
 // ------------------------------------------------------------------ host side
+static int pow2_ceil(long x) {
+    int p = 1;
+    while (p < x && p < (1 << 30)) p <<= 1;
+    return p;
+}
+
 DecodePlan decode_plan(int n_seq, int HKV, int max_kv) {
-    // Smallest chunk (multiple of the 64-key sub-tile) that keeps the split count within
-    // the combine's LDS table and the total grid (empty splits included) bounded.
-    int chunk = kSub;
-    for (;;) {
-        const long ns = ((long)max_kv + chunk - 1) / chunk;
-        if (ns <= kDecodeMaxSplits && (long)n_seq * HKV * ns <= 32768) break;
-        chunk *= 2;
+    // Aim at about one workgroup per CU (256 CUs): chunk = keys per workgroup, a power of
+    // two in [128, 2048] (128 fills every wave's two-tile ring once); the split count
+    // stays within the combine's LDS table.
+    const long rows = (long)max_kv * n_seq * HKV;
+    int chunk = pow2_ceil((rows + 255) / 256);
+    if (chunk < 128) chunk = 128;
+    if (chunk > 2048) chunk = 2048;
+    if (const char* env = std::getenv("EI_DECODE_CHUNK")) {  // tuning override (multiple of 64)
+        const int v = std::atoi(env);
+        if (v >= 64 && v % 64 == 0) chunk = v;
     }
+    while (((long)max_kv + chunk - 1) / chunk > kDecodeMaxSplits) chunk *= 2;
     DecodePlan p;
     p.chunk = chunk;
     p.nsplit = (max_kv + chunk - 1) / chunk;
@@ -395,25 +497,40 @@ size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv) {
     const DecodePlan p = decode_plan(n_seq, HKV, max_kv);
     const size_t slots = (size_t)n_seq * HKV * p.nsplit;
     const int G = H / HKV;
-    return align256(slots * G * kHeadDim * 4) + align256(slots * G * 2 * 4) + align256((size_t)n_seq * HKV * 4);
+    return align256(slots * G * kHeadDim * 4) + align256(slots * G * 2 * 4);
+}
+
+template <int G, int NW>
+static hipError_t launch_gw(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused) {
+    const dim3 grid(a.nsplit, a.HKV, n_seq);
+    const size_t lds = (size_t)kRingTiles * kTileFloats * sizeof(float);  // 128 KB
+    static bool opted[2] = {false, false};
+    if (!opted[fused]) {
+        const void* f = fused ? (const void*)k_decode<G, true, NW> : (const void*)k_decode<G, false, NW>;
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        opted[fused] = true;
+    }
+    if (fused) k_decode<G, true, NW><<<grid, 64 * NW, lds, st>>>(a);
+    else k_decode<G, false, NW><<<grid, 64 * NW, lds, st>>>(a);
+    if (a.nsplit > 1) k_combine<G><<<n_seq * a.H, 128, 0, st>>>(a);
+    return hipGetLastError();
 }
 
 template <int G>
-static void launch_g(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused) {
-    const dim3 grid(a.nsplit, a.HKV, n_seq);
-    if (fused) k_decode<G, true><<<grid, kThreads, 0, st>>>(a);
-    else k_decode<G, false><<<grid, kThreads, 0, st>>>(a);
+static hipError_t launch_g(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused) {
+    // one tile per wave with 8 waves when the chunk is short, else 4 waves streaming
+    return a.chunk <= 8 * kTile ? launch_gw<G, 8>(st, a, n_seq, fused) : launch_gw<G, 4>(st, a, n_seq, fused);
 }
 
 hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused) {
     switch (a.H / a.HKV) {
-        case 1: launch_g<1>(st, a, n_seq, fused); break;
-        case 2: launch_g<2>(st, a, n_seq, fused); break;
-        case 4: launch_g<4>(st, a, n_seq, fused); break;
-        case 8: launch_g<8>(st, a, n_seq, fused); break;
+        case 1: return launch_g<1>(st, a, n_seq, fused);
+        case 2: return launch_g<2>(st, a, n_seq, fused);
+        case 4: return launch_g<4>(st, a, n_seq, fused);
+        case 8: return launch_g<8>(st, a, n_seq, fused);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes) {

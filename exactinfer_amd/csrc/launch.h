@@ -44,7 +44,6 @@ struct DecodeArgs {
     int chunk, nsplit;
     float* part_acc;        // [n_seq*HKV*nsplit][G][128]
     float* part_ml;         // [n_seq*HKV*nsplit][G][2]
-    unsigned* counters;     // [n_seq*HKV]
     // fused prologue
     const float* q_gamma;
     const float* k_gamma;

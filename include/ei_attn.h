@@ -80,11 +80,11 @@ int ei_qkv_prepare(ei_stream_t stream, float* qkv, int rows, long row_stride, in
 
 /* ------------------------------------------------------------------ decode (split-K)
  * Workspace for the decode entry points: per (sequence, kv head, key split) partial
- * (m, l, acc) plus one arrival counter per (sequence, kv head).  max_kv bounds the number
- * of visible keys of any sequence over the workspace's life (it fixes the split grid, so
- * a captured graph stays valid as positions advance).  The workspace must be cleared once
- * with ei_attn_workspace_init before first use; every decode call leaves it cleared
- * again.  Calls that share a workspace must not overlap in time. */
+ * (m, l, acc).  max_kv bounds the number of visible keys of any sequence over the
+ * workspace's life (it fixes the split grid, so a captured graph stays valid as positions
+ * advance).  The contents are scratch: no initialisation is required
+ * (ei_attn_workspace_init zero-fills it, with a kernel rather than a memset, and is
+ * optional).  Calls that share a workspace must not overlap in time. */
 size_t ei_attn_decode_ws_bytes(int n_seq, int n_head, int n_head_kv, int max_kv);
 int ei_attn_workspace_init(ei_stream_t stream, void* ws, size_t ws_bytes);
 
@@ -105,8 +105,8 @@ int ei_attn_decode_batched(ei_stream_t stream, const float* q, long q_stride, fl
                            const float* vc, const int64_t* kv_offset, const int* kv_len, int n_seq, int n_head,
                            int n_head_kv, int head_dim, float scale, int max_kv, void* ws, size_t ws_bytes);
 
-/* Fused decode step: one launch doing ei_qkv_prepare + ei_attn_decode for one token per
- * sequence.  qkv row s (at qkv + s*row_stride, [Q|K|V] raw projections) is read only;
+/* Fused decode step: ei_qkv_prepare + ei_attn_decode for one token per sequence in one
+ * decode launch (plus the small split-combine launch when the keys are split).  qkv row s (at qkv + s*row_stride, [Q|K|V] raw projections) is read only;
  * the normed+roped K row and the V row are written to cache row kv_offset[s] + pos_s,
  * pos_s = kv_len[s]-1 (or *pos_dev when kv_len is NULL; then n_seq must be 1 and
  * kv_offset may be NULL).  out [n_seq][n_head][128].  Equivalent to the per-layer
