@@ -25,6 +25,11 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by
+# the factor a plain 256 MiB copy needs (FETCH x2.000, WRITE x1.000); profiles/*_hbm_traffic.md
+# and profiles/prefill_configs2_kernel_trace.md hold the runs.
+TRAFFIC_DECODE_PER_LAYER = (16546 + 306.5) * 2.0 * 1024 + (528 + 16) * 1024  # k_decode + k_combine
+TRAFFIC_PREFILL = 24692 * 2.0 * 1024 + 32768 * 1024                          # k_prefill
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 D = 128
 
@@ -43,6 +48,8 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="launch the per-layer kernels eagerly")
     ap.add_argument("--extra", action="store_true", help="also measure configs[3] and configs[4]")
     ap.add_argument("--only", choices=["decode", "prefill", "longctx", "batched"], default=None)
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
     return ap.parse_args()
 
 
@@ -281,6 +288,15 @@ def main():
     from exactinfer_amd import attention as A
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
+    if args.calib_copy:
+        n = args.calib_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": n * 4}))
+        return
     use_graph = not args.no_graph
     res = {}
     if args.only in (None, "decode"):
@@ -323,8 +339,8 @@ def main():
                                "36 launches per step in one HIP graph" if dec["graph"] else "eager launches",
                    "pct_hbm_peak": round(100 * dec["gbs"] / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(dec["kernel_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_decode<4,true>", "kernel_us": round(dec["kernel_ms"] * 1e3, 3),
+                     "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_DECODE_PER_LAYER,
+                     "kernel": "k_decode<4,true,8> + k_combine<4> (one layer)", "kernel_us": round(dec["kernel_ms"] * 1e3, 3),
                      "bytes_per_launch": dec["bytes_per_launch"]},
         "cpu_baseline": cpu,
     }
@@ -335,7 +351,7 @@ def main():
                            "roofline": {"bound": "mfma", "achieved": round(pre["kernel_tflops"], 3),
                                         "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                                         "frac": round(pre["kernel_tflops"] / FP32_MFMA_PEAK_TFLOPS, 4),
-                                        "traffic": None, "kernel": "k_prefill<4>",
+                                        "traffic": TRAFFIC_PREFILL, "kernel": "k_prefill<4>",
                                         "kernel_us": round(pre["kernel_ms"] * 1e3, 2),
                                         "flops_per_launch": pre["flops_per_launch"]}}
     for k in ("longctx", "batched"):

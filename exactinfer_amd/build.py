@@ -15,7 +15,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libei_attn.so"
-SOURCES = ["prologue.hip", "decode.hip", "prefill.hip", "capi.cpp"]
+SOURCES = ["csrc/prologue.hip", "csrc/decode.hip", "csrc/prefill.hip", "csrc/capi.cpp", "host/hip_attention.cpp"]
 HEADERS = ["common.h", "launch.h"]
 
 HIPCC_FLAGS = [
@@ -41,7 +41,7 @@ def hipcc() -> str:
 def build(verbose: bool = False) -> Path:
     """Compile every source for gfx950 into exactinfer_amd/libei_attn.so (always rebuilds)."""
     cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(ROOT / "include"),
-           *[str(CSRC / s) for s in SOURCES], "-o", str(LIB) + ".tmp"]
+           *[str(PKG / s) for s in SOURCES], "-o", str(LIB) + ".tmp"]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

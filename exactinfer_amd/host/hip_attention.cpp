@@ -1,0 +1,101 @@
+// hip_attention.cpp — HipAttention: the attention part of a HIP backend (see the header).
+#include "hip_attention.h"
+
+#include <cmath>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/ei_attn.h"
+
+namespace ei {
+
+namespace {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string("HIP error (") + what + "): " + hipGetErrorString(e));
+}
+
+}  // namespace
+
+void HipAttention::check(int status) const {
+    if (status != EI_OK) throw std::runtime_error(std::string("attention kernel call failed: ") + ei_last_error());
+}
+
+HipAttention::HipAttention(const AttnConfig& cfg, int n_ctx, int max_batch, hipStream_t stream)
+    : c_(cfg), n_ctx_(n_ctx), max_batch_(max_batch), stream_(stream) {
+    if (n_ctx_ <= 0) throw std::runtime_error("n_ctx must be positive");
+    if (max_batch_ <= 0) throw std::runtime_error("max_batch must be positive");
+    if (c_.n_layer <= 0 || c_.n_head <= 0 || c_.n_head_kv <= 0 || c_.n_head % c_.n_head_kv)
+        throw std::runtime_error("invalid attention configuration");
+    if (c_.head_dim != 128) throw std::runtime_error("the HIP path supports head_dim = 128 only");
+    // scale as the reference computes it (src/model.cpp:163, src/cuda/model_cuda.cu:1786)
+    scale_ = 1.0f / std::sqrt(float(c_.head_dim));
+
+    const size_t kd = size_t(c_.n_head_kv) * c_.head_dim;
+    const size_t per_cache = size_t(c_.n_layer) * size_t(n_ctx_) * kd * sizeof(float);
+    hip_check(hipMalloc(&kv_, 2 * per_cache), "KV cache");
+    hip_check(hipMemsetAsync(kv_, 0, 2 * per_cache, stream_), "KV cache clear");
+
+    std::vector<float> cs(size_t(n_ctx_) * size_t(c_.rope_dim));
+    check(ei_rope_table_fill(cs.data(), n_ctx_, c_.rope_dim, c_.rope_base));
+    hip_check(hipMalloc(&rope_, cs.size() * sizeof(float)), "RoPE table");
+    hip_check(hipMemcpy(rope_, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice), "RoPE upload");
+
+    ws_bytes_ = ei_attn_decode_ws_bytes(1, c_.n_head, c_.n_head_kv, n_ctx_);
+    if (ws_bytes_ == 0) throw std::runtime_error("decode workspace size");
+    hip_check(hipMalloc(&ws_, ws_bytes_), "decode workspace");
+    check(ei_attn_workspace_init(stream_, ws_, ws_bytes_));
+
+    hip_check(hipMalloc(&pos_dev_, sizeof(int)), "position");
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&pos_host_), sizeof(int), hipHostMallocDefault), "pinned position");
+    hip_check(hipStreamSynchronize(stream_), "init");
+}
+
+HipAttention::~HipAttention() {
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (pos_host_) (void)hipHostFree(pos_host_);
+    if (pos_dev_) (void)hipFree(pos_dev_);
+    if (ws_) (void)hipFree(ws_);
+    if (rope_) (void)hipFree(rope_);
+    if (kv_) (void)hipFree(kv_);
+}
+
+void HipAttention::begin_chunk(int pos0, int B) {
+    if (B <= 0) throw std::invalid_argument("empty chunk");
+    if (B > max_batch_) throw std::invalid_argument("chunk larger than max_batch");
+    if (pos0 < 0 || pos0 + B > n_ctx_) throw std::out_of_range("context window full");
+    // the pinned host word is reused: wait until the previous chunk's upload has been consumed
+    hip_check(hipStreamSynchronize(stream_), "chunk sync");
+    *pos_host_ = pos0;
+    hip_check(hipMemcpyAsync(pos_dev_, pos_host_, sizeof(int), hipMemcpyHostToDevice, stream_), "position upload");
+    B_ = B;
+}
+
+float* HipAttention::kcache(int l) const {
+    const size_t kd = size_t(c_.n_head_kv) * c_.head_dim;
+    return kv_ + size_t(l) * size_t(n_ctx_) * kd;
+}
+
+float* HipAttention::vcache(int l) const {
+    const size_t kd = size_t(c_.n_head_kv) * c_.head_dim;
+    return kv_ + (size_t(c_.n_layer) + size_t(l)) * size_t(n_ctx_) * kd;
+}
+
+void HipAttention::layer(int l, float* qkv, long qkv_stride, const float* q_norm, const float* k_norm, float* att) {
+    if (l < 0 || l >= c_.n_layer) throw std::out_of_range("layer index");
+    if (B_ <= 0) throw std::logic_error("layer() before begin_chunk()");
+    const int H = c_.n_head, HKV = c_.n_head_kv, D = c_.head_dim;
+    if (B_ == 1) {
+        // decode: one fused launch (+ split merge), cache row *pos written in place
+        check(ei_decode_step(stream_, qkv, qkv_stride, att, kcache(l), vcache(l), nullptr, nullptr, pos_dev_, 1, H,
+                             HKV, D, q_norm, k_norm, rope_, c_.rope_dim, c_.eps, scale_, n_ctx_, ws_, ws_bytes_));
+    } else {
+        // prompt chunk: QK-norm + RoPE + append for all B rows, then causal attention over
+        // cache rows 0..pos0+b (earlier chunks included)
+        check(ei_qkv_prepare(stream_, qkv, B_, qkv_stride, H, HKV, D, q_norm, k_norm, rope_, pos_dev_, c_.rope_dim,
+                             c_.eps, kcache(l), vcache(l)));
+        check(ei_attn_prefill(stream_, qkv, qkv_stride, att, kcache(l), vcache(l), pos_dev_, B_, H, HKV, D, scale_));
+    }
+}
+
+}  // namespace ei

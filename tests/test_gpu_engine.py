@@ -1,0 +1,37 @@
+"""Engine-level parity: the C++ HipAttention (exactinfer_amd/host/) driven like the reference
+engine drives attention — prompt chunks, then one-token decode steps, every layer — against
+the CPU oracle processing the same tokens one at a time.  Runs the compiled driver
+tests/cpp/engine_test as a subprocess, as the reference's own tests drive its binary."""
+import json
+import subprocess
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+EXE = Path(__file__).resolve().parent / "cpp" / "engine_test"
+
+
+def _run(*args):
+    if not EXE.exists():
+        pytest.fail(f"{EXE} not built (run __graft_entry__.build())")
+    r = subprocess.run([str(EXE), *map(str, args)], capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr)
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    return r.returncode, res
+
+
+def test_config0_prefill512_decode128():
+    """0.6B heads (16/8), one layer, 512-token prefill then 128 decode
+    steps, each appending to the KV cache."""
+    rc, res = _run(1, 16, 8, 512, 512, 128, 640)
+    assert rc == 0 and res["ok"], res
+    assert res["caches_bit_exact"] and res["out_of_range_thrown"]
+
+
+def test_chunked_prompt_crosses_chunk_boundaries():
+    """Prompt evaluated in 128-token chunks (pos0 > 0 for later chunks, the case the
+    reference's attn_long test covers), 4B heads, two layers, then decode steps."""
+    rc, res = _run(2, 32, 8, 300, 128, 12, 400)
+    assert rc == 0 and res["ok"], res

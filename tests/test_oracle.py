@@ -235,3 +235,32 @@ def test_batched_equals_per_sequence(orc):
     for s in range(4):
         ref = orc.attn_decode(q[s].reshape(H, D), k[offs[s]:], v[offs[s]:], int(lens[s]), H, HKV, D)
         assert bits_equal(out[s], ref)
+
+
+# ---------------------------------------------------------------- golden fixtures
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+def test_oracle_matches_reference_golden_vectors(orc):
+    """Vectors produced by the reference's own rmsnorm / rope_inv_freq / rope (compiled from
+    its sources; tests/golden/make_golden.py): the oracle reproduces every one bit for bit."""
+    g = np.load(GOLDEN / "ref_qknorm_rope.npz")
+    eps = float(g["eps"][0])
+    for i in range(g["x"].shape[0]):
+        assert bits_equal(orc.rmsnorm(g["x"][i], g["gamma"][i], eps), g["rmsnorm"][i])
+    for rd, base in ((128, 1e6), (64, 1e4)):
+        f = orc.rope_inv_freq(rd, base)
+        assert np.array_equal(f, g[f"inv_freq_{rd}_{int(base)}"])
+        for i, p in enumerate(g["pos"]):
+            assert bits_equal(orc.rope(g[f"rope_in_{rd}_{int(base)}"][i], int(p), f),
+                              g[f"rope_out_{rd}_{int(base)}"][i])
+
+
+def test_oracle_attention_regression_fixture(orc):
+    a = np.load(GOLDEN / "attn_small.npz")
+    for name in ("gqa4_t1", "gqa2_t37", "gqa4_t300"):
+        H, HKV, T = (int(x) for x in a[f"{name}_shape"])
+        sq, sk, sv = (int(x) for x in a[f"{name}_seeds"])
+        q, k, v = orc.normal((H, D), sq), orc.normal((T, HKV, D), sk), orc.normal((T, HKV, D), sv)
+        out = orc.attn_decode(q, k, v, T, H, HKV, D)
+        assert rel_err(out, a[f"{name}_f64"]) <= ATTN_RTOL
