@@ -11,7 +11,10 @@ from pathlib import Path
 
 import torch  # noqa: F401  (must precede the library load, see module docstring)
 
-LIB_PATH = Path(__file__).resolve().parent / "libei_attn.so"
+import os
+
+# EI_ATTN_LIB may point at an alternative build of the same library (e.g. an instrumented one)
+LIB_PATH = Path(os.environ.get("EI_ATTN_LIB") or Path(__file__).resolve().parent / "libei_attn.so")
 
 # every symbol include/ei_attn.h declares (checked by tests/test_capi_exports.py)
 EXPORTS = (

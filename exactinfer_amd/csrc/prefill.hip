@@ -33,6 +33,7 @@ constexpr int kKT = 32;           // keys per tile
 constexpr int kKS = kHeadDim + 4;  // K row stride in LDS (floats): conflict-free row-wise b128 reads
 constexpr int kVS = kHeadDim + 8;  // V row stride in LDS: the two half-waves hit disjoint banks
 constexpr int kTileFloats = kKT * kKS + kKT * kVS;
+constexpr int kBufs = 3;  // LDS tile buffers (software pipeline depth)
 
 template <int GW>
 __global__ __launch_bounds__(64 * GW) void k_prefill(const float* __restrict__ q, long q_stride,
@@ -41,7 +42,7 @@ __global__ __launch_bounds__(64 * GW) void k_prefill(const float* __restrict__ q
                                                      int B, int H, int HKV, int GG, float scale) {
     constexpr int D = kHeadDim;
     constexpr int NT = 64 * GW;
-    extern __shared__ __align__(16) float smem[];  // 2 x [K tile | V tile]
+    extern __shared__ __align__(16) float smem[];  // kBufs x [K tile | V tile]
 
     const int L = blockIdx.x;
     const int kvh = L % HKV;
@@ -108,8 +109,7 @@ __global__ __launch_bounds__(64 * GW) void k_prefill(const float* __restrict__ q
                 }
             }
         };
-        auto stash = [&](int buf) {
-            float* Ks = smem + buf * kTileFloats;
+        auto stash = [&](float* Ks) {
             float* Vs = Ks + kKT * kKS;
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
@@ -119,51 +119,50 @@ __global__ __launch_bounds__(64 * GW) void k_prefill(const float* __restrict__ q
             }
         };
 
-        __syncthreads();  // previous pass finished reading both buffers
-        fetch(0);
-        stash(0);
-        __syncthreads();
+        auto tile = [&](int kt) { return smem + (kt % kBufs) * kTileFloats; };
+        const float sl2 = scale * 1.44269504088896340736f;  // scores in the exp2 domain
 
-        for (int kt = 0; kt < ntile; ++kt) {
-            const int buf = kt & 1;
-            if (kt + 1 < ntile) fetch(kt + 1);
-            const float* Ks = smem + buf * kTileFloats;
-            const float* Vs = Ks + kKT * kKS;
-
-            // ---- S^T = K . Q^T over d = hh*64 + kk
-            floatx16 s;
+        // S^T = K . Q^T over d = hh*64 + kk for the K tile at Ks; the K operand of step
+        // k4+1 is read while the four MFMAs of step k4 run
+        auto qk = [&](const float* Ks) {
+            floatx16 acc;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[i] = 0.f;
+            for (int i = 0; i < 16; ++i) acc[i] = 0.f;
             const float* krow = Ks + col * kKS + hh * 64;
+            float4 kv = *reinterpret_cast<const float4*>(krow);
 #pragma unroll
             for (int k4 = 0; k4 < 16; ++k4) {
-                const float4 kv = *reinterpret_cast<const float4*>(krow + 4 * k4);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * k4 + 0], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qreg[4 * k4 + 1], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qreg[4 * k4 + 2], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qreg[4 * k4 + 3], s, 0, 0, 0);
+                const float4 kn = *reinterpret_cast<const float4*>(krow + 4 * ((k4 + 1) & 15));
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * k4 + 0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qreg[4 * k4 + 1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qreg[4 * k4 + 2], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qreg[4 * k4 + 3], acc, 0, 0, 0);
+                kv = kn;
             }
-
-            // ---- causal mask + online softmax; key of register r: kt*32 + 8(r/4) + 4hh + r%4
+            return acc;
+        };
+        // causal mask + online softmax of one score tile (VALU only): p replaces s, the
+        // running (m, lsum) advance and O is rescaled.  Key of register r:
+        // kt*32 + 8(r/4) + 4hh + r%4.
+        auto softmax = [&](floatx16& sc, int kt) {
             const int kbase_t = kt * kKT + 4 * hh;
-            const bool full = kt * kKT + kKT - 1 <= pos0 + qb * kQB;  // whole tile visible to every query
             float mx = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = kbase_t + 8 * (r >> 2) + (r & 3);
-                const float sv = (full || key <= qpos) ? s[r] * scale : -INFINITY;
-                s[r] = sv;
+                const float sv = key <= qpos ? sc[r] * sl2 : -INFINITY;
+                sc[r] = sv;
                 mx = fmaxf(mx, sv);
             }
             mx = fmaxf(mx, lane_xor32(mx));
             const float mn = fmaxf(m, mx);
             const float base = mn == -INFINITY ? 0.f : mn;  // fully masked so far: keep exp finite
-            const float corr = expf(m - base);
+            const float corr = __builtin_amdgcn_exp2f(m - base);
             float ps = 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                s[r] = expf(s[r] - base);
-                ps += s[r];
+                sc[r] = __builtin_amdgcn_exp2f(sc[r] - base);
+                ps += sc[r];
             }
             lsum = lsum * corr + ps;
             m = mn;
@@ -171,19 +170,51 @@ __global__ __launch_bounds__(64 * GW) void k_prefill(const float* __restrict__ q
             for (int db = 0; db < 4; ++db)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) o[db][i] *= corr;
-
-            // ---- O^T += V^T . P^T; contraction step r pairs keys 8(r/4) + r%4 (+4 for hh=1)
+        };
+        // O^T += V^T . P^T; contraction step r pairs keys 8(r/4) + r%4 (+4 for hh = 1)
+        auto pv = [&](const floatx16& p, const float* Vs) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float* vrow = Vs + (8 * (r >> 2) + 4 * hh + (r & 3)) * kVS + col;
 #pragma unroll
                 for (int db = 0; db < 4; ++db)
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * db], s[r], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * db], p[r], o[db], 0, 0, 0);
             }
+        };
 
-            if (kt + 1 < ntile) stash(buf ^ 1);
-            __syncthreads();
+        // three LDS tile buffers: at step kt the V half of tile kt and the K half of tile
+        // kt+1 are read while tile kt+2 is written; tile kt+3 travels in registers
+        __syncthreads();  // previous pass finished reading every buffer
+        fetch(0);
+        stash(tile(0));
+        if (ntile > 1) {
+            fetch(1);
+            stash(tile(1));
         }
+        __syncthreads();
+        if (ntile > 2) fetch(2);
+        floatx16 s = qk(tile(0));
+
+        for (int kt = 0; kt + 1 < ntile; ++kt) {
+            // one basic block: the next tile's score MFMAs are interleaved with this
+            // tile's softmax VALU work, then this tile's P.V MFMAs
+            const floatx16 s_next = qk(tile(kt + 1));
+            softmax(s, kt);
+            pv(s, tile(kt) + kKT * kKS);
+            // issue order: per K step 1 LDS read, 4 MFMAs, 8 VALU ops
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+            }
+            if (kt + 2 < ntile) stash(tile(kt + 2));
+            __syncthreads();
+            if (kt + 3 < ntile) fetch(kt + 3);
+            s = s_next;
+        }
+        softmax(s, ntile - 1);
+        pv(s, tile(ntile - 1) + kKT * kKS);
 
         // ---- normalise and store: O^T register r of block db is d = 32db + 8(r/4) + 4hh + r%4
         lsum += lane_xor32(lsum);
@@ -212,7 +243,7 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
     const int nb = (B + kQB - 1) / kQB;
     const int npairs = (nb + 1) / 2;
     const unsigned grid = (unsigned)npairs * HKV * GG;
-    const size_t lds = 2 * kTileFloats * sizeof(float);  // > 64 KB: opt in once per instantiation
+    const size_t lds = kBufs * kTileFloats * sizeof(float);  // > 64 KB: opt in once per instantiation
     static bool opted[3] = {false, false, false};
     const int oi = GW == 1 ? 0 : GW == 2 ? 1 : 2;
     if (!opted[oi]) {
