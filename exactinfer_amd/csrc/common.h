@@ -32,6 +32,17 @@ __device__ __forceinline__ float lane_xor16(float v) {
 }
 __device__ __forceinline__ float lane_xor32(float v) { return __shfl_xor(v, 32); }
 
+// Half-wave reductions with v_permlane32_swap: after the swap each lane holds its own value
+// and that of lane ^ 32 (in some order), so a symmetric combine needs no ordering.
+__device__ __forceinline__ float half_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <int M>
 __device__ __forceinline__ float lane_xor(float v) {
     if constexpr (M == 1) return lane_xor1(v);
@@ -64,6 +75,27 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
     return v;
+}
+
+// ------------------------------------------------------------------ LDS DMA
+// LDS byte address of a __shared__ object (the low 32 bits of its flat address).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>(p);
+}
+
+// One LDS-DMA instruction: every active lane copies 16 bytes from its global address to
+// LDS byte address m0_base + 16*lane.  Issued through inline asm so the compiler does not
+// see a pending LDS write and serialise unrelated LDS accesses behind it; completion is
+// tracked by hand with wait_vmcnt (each instruction counts one in vmcnt).
+__device__ __forceinline__ void dma16(const float* g, uint32_t m0_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0_base) : "memory", "m0");
+}
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at 15:14,
+// expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 // ------------------------------------------------------------------ QK-norm + RoPE of one head

@@ -99,19 +99,6 @@ __device__ __forceinline__ float dot4(const float4 a, const float4 b, float acc)
     return fmaf(a.w, b.w, acc);
 }
 
-// LDS byte address of a __shared__ object (the low 32 bits of its flat address).
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)reinterpret_cast<uintptr_t>(p);
-}
-
-// One LDS-DMA instruction: every active lane copies 16 bytes from its global address to
-// LDS byte address m0_base + 16*lane.  Issued through inline asm so the compiler does not
-// see a pending LDS write and serialise unrelated LDS accesses behind it; completion is
-// tracked by hand with wait_vmcnt (each instruction counts one in vmcnt).
-__device__ __forceinline__ void dma16(const float* g, uint32_t m0_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0_base) : "memory", "m0");
-}
-
 // Copy nbytes (<= 1024, multiple of 16) of contiguous global memory into LDS; one
 // instruction, lanes past the end idle.
 __device__ __forceinline__ void dma_block(const float* g, uint32_t lds_base, int nbytes, int lane) {
@@ -146,12 +133,6 @@ __device__ __forceinline__ void issue_tile(const float* slot, const float* kbase
     }
 }
 
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at 15:14,
-// expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 // NW waves per workgroup, each with a ring of kRingTiles/NW tile slots: 4 waves x 2 slots
 // streams long chunks with one tile always in flight behind the one being scored; 8 waves

@@ -8,15 +8,32 @@
 // so that in the 32x32 accumulator layout every lane owns ONE query column and 16 key
 // rows: the row max / row sum of the softmax need only the lane's own 16 values plus one
 // exchange with lane^32.  The same registers, unchanged, are the B operand of
-//     O^T[d][query] = V^T . P^T          (A = V columns from LDS)
+//     O^T[d][query] = V^T . P^T          (A = V from LDS)
 // because the accumulator row order (8*(r/4) + 4*(lane/32) + r%4) is used as the
 // contraction order of the second product.  The contraction order over d in the first
-// product is (lane/32)*64 + step, so each lane's Q^T and K operands are 64 contiguous
-// floats of one row.
+// product is (lane/32)*64 + step, so each lane's Q^T operand is 64 contiguous floats.
+// Output block db (0..3) of O^T holds d = 4*i + db for accumulator row i, so the A operand
+// of all four blocks for one key is a single 16-byte LDS read V[key][4*lane .. 4*lane+3].
 //
-// A workgroup holds GW = min(G, 4) waves, the GW query heads of one KV head that share
-// every K/V tile: the tile (32 keys x 128 d of K and of V) is staged once into LDS,
-// double-buffered, with the next tile's global loads in flight during the MFMA work.
+// Workgroup = KS key groups x GW query heads (the GW heads of one KV head that share every
+// K/V tile).  Key group g takes the tiles kt = KS*i + g of the block's causal range and
+// keeps its own (m, l, O); the groups merge through LDS at the end of the block.  With
+// KS = 2 every SIMD runs two waves, so one wave's softmax VALU work and LDS waits overlap
+// the other's matrix instructions.
+//
+// K/V tiles (32 keys) reach LDS by LDS DMA (global_load_lds_dwordx4) straight from the
+// cache, two tiles ahead for K and one for V, per key group:
+//   K tile chunk-major  [32 chunks of 4 d][32 keys][4 floats]: the 32 lanes reading one
+//     d-chunk of 32 different keys touch 512 contiguous bytes (no bank conflicts);
+//   V tile row-major    [32 keys][128 floats].
+// Rows past the causal end are clamped to the last visible row (valid memory, masked out).
+//
+// Softmax runs in the exp2 domain (scores x scale x log2 e, one FMA per score).  The
+// running maximum is raised only when a tile's maximum exceeds it by more than kLazy
+// (log2 units), so P <= 2^kLazy and O / l are rescaled rarely; the result is the same
+// softmax (the common factor cancels in O / l).  The causal mask is applied only on the
+// (at most two) tiles that cross the block's diagonal.
+//
 // Causal balance: query block qb needs qb+1+pos0/32 tiles, so a workgroup runs block p
 // and then block nb-1-p; every workgroup has the same amount of work.  Workgroup id
 // L -> kv head L % HKV first, so with 8 KV heads all blocks of one KV head share an
@@ -28,21 +45,23 @@ namespace ei {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kQB = 32;           // queries per wave (and per block)
-constexpr int kKT = 32;           // keys per tile
-constexpr int kKS = kHeadDim + 4;  // K row stride in LDS (floats): conflict-free row-wise b128 reads
-constexpr int kVS = kHeadDim + 8;  // V row stride in LDS: the two half-waves hit disjoint banks
-constexpr int kTileFloats = kKT * kKS + kKT * kVS;
-constexpr int kBufs = 3;  // LDS tile buffers (software pipeline depth)
+constexpr int kQB = 32;                          // queries per wave (and per block)
+constexpr int kKT = 32;                          // keys per tile
+constexpr int kTileF = kKT * kHeadDim;           // floats in one K or V tile (16 KB)
+constexpr int kGroupF = 4 * kTileF;              // per key group: 2 K + 2 V tile buffers
+constexpr int kKS = 2;                           // key groups per workgroup
+constexpr float kLazy = 8.f;                     // lazy-rescale threshold (log2 units)
+constexpr int kXchF = 34;                        // floats per lane exchanged by the merge
 
 template <int GW>
-__global__ __launch_bounds__(64 * GW) void k_prefill(const float* __restrict__ q, long q_stride,
-                                                     float* __restrict__ out, const float* __restrict__ kc,
-                                                     const float* __restrict__ vc, const int* __restrict__ pos_dev,
-                                                     int B, int H, int HKV, int GG, float scale) {
+__global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restrict__ q, long q_stride,
+                                                           float* __restrict__ out, const float* __restrict__ kc,
+                                                           const float* __restrict__ vc,
+                                                           const int* __restrict__ pos_dev, int B, int H, int HKV,
+                                                           int GG, float scale) {
     constexpr int D = kHeadDim;
-    constexpr int NT = 64 * GW;
-    extern __shared__ __align__(16) float smem[];  // kBufs x [K tile | V tile]
+    constexpr int DMA_PER_WAVE = 16 / GW;  // DMA instructions per wave per K (or V) tile
+    extern __shared__ __align__(16) float smem[];
 
     const int L = blockIdx.x;
     const int kvh = L % HKV;
@@ -51,13 +70,17 @@ __global__ __launch_bounds__(64 * GW) void k_prefill(const float* __restrict__ q
     const int pair = rest / GG;
     const int G = GW * GG;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wu = __builtin_amdgcn_readfirstlane(w);  // wave-uniform: keeps the branches scalar
+    const int hw = wu % GW, grp = wu / GW;
     const int col = lane & 31, hh = lane >> 5;
-    const int h = kvh * G + hg * GW + w;
+    const int h = kvh * G + hg * GW + hw;
     const int pos0 = *pos_dev;
     const size_t KD = (size_t)HKV * D;
     const float* kbase = kc + (size_t)kvh * D;
     const float* vbase = vc + (size_t)kvh * D;
     const int nb = (B + kQB - 1) / kQB;
+    float* gsm = smem + grp * kGroupF;  // this key group's buffers: K0 K1 V0 V1
+    const float sl2 = scale * 1.44269504088896340736f;
 
     for (int pass = 0; pass < 2; ++pass) {
         const int qb = pass == 0 ? pair : nb - 1 - pair;
@@ -89,148 +112,152 @@ __global__ __launch_bounds__(64 * GW) void k_prefill(const float* __restrict__ q
             for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
         float m = -INFINITY, lsum = 0.f;
 
-        const int T = pos0 + min(B, qb * kQB + kQB);  // keys seen by the block's last query
+        const int T = pos0 + min(B, qb * kQB + kQB);   // keys seen by the block's last query
         const int ntile = (T + kKT - 1) / kKT;
+        const int nfull = (pos0 + qb * kQB + 1) / kKT;  // tiles below the diagonal (no mask)
+        const int n_it = (ntile + kKS - 1) / kKS;
+        const int n_mine = (ntile - grp + kKS - 1) / kKS;  // tiles of this key group
 
-        // cooperative tile staging: 32 rows x 32 float4 for K and for V
-        constexpr int PER = kKT * (D / 4) / NT;
-        float4 stk[PER], stv[PER];
-        auto fetch = [&](int kt) {
+        // DMA of this group's i-th tile (kt = KS*i + grp) into a K or V buffer
+        auto dma_k = [&](int i, int buf) {
+            const int t0 = (kKS * i + grp) * kKT;
+            const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsm + buf * kTileF));
 #pragma unroll
-            for (int j = 0; j < PER; ++j) {
-                const int i = tid + NT * j, row = i >> 5, c4 = (i & 31) * 4;
-                const int t = kt * kKT + row;
-                if (t < T) {
-                    stk[j] = *reinterpret_cast<const float4*>(kbase + (size_t)t * KD + c4);
-                    stv[j] = *reinterpret_cast<const float4*>(vbase + (size_t)t * KD + c4);
-                } else {
-                    stk[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    stv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                }
+            for (int j = 0; j < DMA_PER_WAVE; ++j) {
+                const int ins = hw * DMA_PER_WAVE + j;  // 1 KB = d-chunks 2*ins, 2*ins+1
+                const int chunk = 2 * ins + hh;
+                const int key = min(t0 + col, T - 1);
+                dma16(kbase + (size_t)key * KD + 4 * chunk, lb + ins * 1024);
             }
         };
-        auto stash = [&](float* Ks) {
-            float* Vs = Ks + kKT * kKS;
+        auto dma_v = [&](int i, int buf) {
+            const int t0 = (kKS * i + grp) * kKT;
+            const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsm + (2 + buf) * kTileF));
 #pragma unroll
-            for (int j = 0; j < PER; ++j) {
-                const int i = tid + NT * j, row = i >> 5, c4 = (i & 31) * 4;
-                *reinterpret_cast<float4*>(Ks + row * kKS + c4) = stk[j];
-                *reinterpret_cast<float4*>(Vs + row * kVS + c4) = stv[j];
+            for (int j = 0; j < DMA_PER_WAVE; ++j) {
+                const int ins = hw * DMA_PER_WAVE + j;  // 1 KB = keys 2*ins, 2*ins+1
+                const int key = min(t0 + 2 * ins + hh, T - 1);
+                dma16(vbase + (size_t)key * KD + 4 * col, lb + ins * 1024);
             }
         };
 
-        auto tile = [&](int kt) { return smem + (kt % kBufs) * kTileFloats; };
-        const float sl2 = scale * 1.44269504088896340736f;  // scores in the exp2 domain
-
-        // S^T = K . Q^T over d = hh*64 + kk for the K tile at Ks; the K operand of step
-        // k4+1 is read while the four MFMAs of step k4 run
-        auto qk = [&](const float* Ks) {
-            floatx16 acc;
+        // S^T = K . Q^T for the K tile at Kt (chunk-major); the operand of step k4+1 is
+        // read while the four MFMAs of step k4 run
+        auto qk = [&](const float* Kt, floatx16& acc) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-            const float* krow = Ks + col * kKS + hh * 64;
-            float4 kv = *reinterpret_cast<const float4*>(krow);
+            const float* kp = Kt + hh * 16 * (kKT * 4) + col * 4;
+            float4 kv = *reinterpret_cast<const float4*>(kp);
 #pragma unroll
             for (int k4 = 0; k4 < 16; ++k4) {
-                const float4 kn = *reinterpret_cast<const float4*>(krow + 4 * ((k4 + 1) & 15));
+                const float4 kn = *reinterpret_cast<const float4*>(kp + ((k4 + 1) & 15) * (kKT * 4));
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * k4 + 0], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qreg[4 * k4 + 1], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qreg[4 * k4 + 2], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qreg[4 * k4 + 3], acc, 0, 0, 0);
                 kv = kn;
             }
-            return acc;
         };
-        // causal mask + online softmax of one score tile (VALU only): p replaces s, the
-        // running (m, lsum) advance and O is rescaled.  Key of register r:
-        // kt*32 + 8(r/4) + 4hh + r%4.
-        auto softmax = [&](floatx16& sc, int kt) {
-            const int kbase_t = kt * kKT + 4 * hh;
-            float mx = -INFINITY;
+
+        // One tile kt of this group: softmax of its scores s (in place: s becomes P^T) and
+        // O^T += V^T . P^T with V at Vt; when Kn is set the next tile's scores go to sn.
+        auto step = [&](floatx16& s, floatx16& sn, int kt, const float* Kn, const float* Vt) {
+            if (kt >= nfull) {  // tile crosses the diagonal (wave-uniform)
+                const int k0 = kt * kKT + 4 * hh;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kbase_t + 8 * (r >> 2) + (r & 3);
-                const float sv = key <= qpos ? sc[r] * sl2 : -INFINITY;
-                sc[r] = sv;
-                mx = fmaxf(mx, sv);
+                for (int r = 0; r < 16; ++r)
+                    if (k0 + 8 * (r >> 2) + (r & 3) > qpos) s[r] = -INFINITY;
             }
-            mx = fmaxf(mx, lane_xor32(mx));
-            const float mn = fmaxf(m, mx);
-            const float base = mn == -INFINITY ? 0.f : mn;  // fully masked so far: keep exp finite
-            const float corr = __builtin_amdgcn_exp2f(m - base);
-            float ps = 0.f;
+            float mx = s[0];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                sc[r] = __builtin_amdgcn_exp2f(sc[r] - base);
-                ps += sc[r];
-            }
-            lsum = lsum * corr + ps;
-            m = mn;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[db][i] *= corr;
-        };
-        // O^T += V^T . P^T; contraction step r pairs keys 8(r/4) + r%4 (+4 for hh = 1)
-        auto pv = [&](const floatx16& p, const float* Vs) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float* vrow = Vs + (8 * (r >> 2) + 4 * hh + (r & 3)) * kVS + col;
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+            const float ms = half_max(mx) * sl2;
+            if (__builtin_amdgcn_ballot_w64(ms > m + kLazy)) {  // rare after the first tile
+                const float mn = fmaxf(m, ms);
+                const float corr = m == mn ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+                lsum *= corr;
 #pragma unroll
                 for (int db = 0; db < 4; ++db)
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * db], p[r], o[db], 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) o[db][i] *= corr;
+                m = mn;
+            }
+            const float nb_ = m == -INFINITY ? 0.f : -m;
+            if (Kn) qk(Kn, sn);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], sl2, nb_));
+                lsum += s[r];
+            }
+            const float* vp = Vt + 4 * hh * D + 4 * col;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float4 vv = *reinterpret_cast<const float4*>(vp + (8 * (r >> 2) + (r & 3)) * D);
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, s[r], o[0], 0, 0, 0);
+                o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, s[r], o[1], 0, 0, 0);
+                o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, s[r], o[2], 0, 0, 0);
+                o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, s[r], o[3], 0, 0, 0);
             }
         };
 
-        // three LDS tile buffers: at step kt the V half of tile kt and the K half of tile
-        // kt+1 are read while tile kt+2 is written; tile kt+3 travels in registers
-        __syncthreads();  // previous pass finished reading every buffer
-        fetch(0);
-        stash(tile(0));
-        if (ntile > 1) {
-            fetch(1);
-            stash(tile(1));
+        // K buffers hold tiles i (even i in K0) and i+1; V buffers tile i.  At iteration
+        // i: DMA K(i+2) -> K[i%2] and V(i+1) -> V[(i+1)%2] (both last read in iteration
+        // i-1), read K(i+1) and V(i) (both landed by the wait + barrier ending i-1).
+        // The score tiles alternate between sa and sb (loop unrolled by two).
+        __syncthreads();  // previous pass (or merge) finished with every buffer
+        if (n_mine > 0) {
+            dma_k(0, 0);
+            dma_v(0, 0);
+        }
+        if (n_mine > 1) dma_k(1, 1);
+        wait_vmcnt<0>();
+        __syncthreads();
+        floatx16 sa, sb;
+        if (n_mine > 0) qk(gsm, sa);
+        auto iter = [&](int i, floatx16& s, floatx16& sn) {
+            if (i + 2 < n_mine) dma_k(i + 2, i & 1);
+            if (i + 1 < n_mine) dma_v(i + 1, (i + 1) & 1);
+            if (i < n_mine)
+                step(s, sn, kKS * i + grp, i + 1 < n_mine ? gsm + ((i + 1) & 1) * kTileF : nullptr,
+                     gsm + (2 + (i & 1)) * kTileF);
+            wait_vmcnt<0>();
+            __syncthreads();
+        };
+        for (int i = 0; i < n_it; i += 2) {
+            iter(i, sa, sb);
+            if (i + 1 < n_it) iter(i + 1, sb, sa);
+        }
+
+        // ---- merge the key groups through LDS (tile buffers are free after the barrier):
+        // group g finalises output blocks db = 2g, 2g+1 and hands the other two to its partner
+        float* xw = smem + w * (kXchF * 64) + lane;
+        xw[0] = m;
+        xw[64] = lsum;
+        // (grp is wave-uniform: selects, not a dynamic register index)
+        const floatx16 give0 = grp ? o[0] : o[2], give1 = grp ? o[1] : o[3];
+        const floatx16 keep0 = grp ? o[2] : o[0], keep1 = grp ? o[3] : o[1];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            xw[(2 + i) * 64] = give0[i];
+            xw[(18 + i) * 64] = give1[i];
         }
         __syncthreads();
-        if (ntile > 2) fetch(2);
-        floatx16 s = qk(tile(0));
-
-        for (int kt = 0; kt + 1 < ntile; ++kt) {
-            // one basic block: the next tile's score MFMAs are interleaved with this
-            // tile's softmax VALU work, then this tile's P.V MFMAs
-            const floatx16 s_next = qk(tile(kt + 1));
-            softmax(s, kt);
-            pv(s, tile(kt) + kKT * kKS);
-            // issue order: per K step 1 LDS read, 4 MFMAs, 8 VALU ops
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-            }
-            if (kt + 2 < ntile) stash(tile(kt + 2));
-            __syncthreads();
-            if (kt + 3 < ntile) fetch(kt + 3);
-            s = s_next;
-        }
-        softmax(s, ntile - 1);
-        pv(s, tile(ntile - 1) + kKT * kKS);
-
-        // ---- normalise and store: O^T register r of block db is d = 32db + 8(r/4) + 4hh + r%4
-        lsum += lane_xor32(lsum);
+        const float* xp = smem + ((1 - grp) * GW + hw) * (kXchF * 64) + lane;
+        const float mp = xp[0], lp = xp[64];
+        const float mt = fmaxf(m, mp);  // finite: key 0 is visible to every lane
+        const float c0 = __builtin_amdgcn_exp2f(m - mt), cp = __builtin_amdgcn_exp2f(mp - mt);
+        const float l = half_sum(lsum * c0 + lp * cp);
+        const float inv = 1.f / l;
         if (b < B) {
-            float* dst = out + ((size_t)b * H + h) * D + 4 * hh;
+            // O^T register r of block db is d = 4*(8(r/4) + 4hh + r%4) + db
+            float* dst = out + ((size_t)b * H + h) * D + 16 * hh + 2 * grp;
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int r4 = 0; r4 < 4; ++r4) {
-                    float4 v;
-                    v.x = o[db][4 * r4 + 0] / lsum;
-                    v.y = o[db][4 * r4 + 1] / lsum;
-                    v.z = o[db][4 * r4 + 2] / lsum;
-                    v.w = o[db][4 * r4 + 3] / lsum;
-                    *reinterpret_cast<float4*>(dst + 32 * db + 8 * r4) = v;
-                }
+            for (int r = 0; r < 16; ++r) {
+                float2 v;
+                v.x = (keep0[r] * c0 + xp[(2 + r) * 64] * cp) * inv;
+                v.y = (keep1[r] * c0 + xp[(18 + r) * 64] * cp) * inv;
+                *reinterpret_cast<float2*>(dst + 4 * (8 * (r >> 2) + (r & 3))) = v;
+            }
         }
     }
 }
@@ -243,7 +270,8 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
     const int nb = (B + kQB - 1) / kQB;
     const int npairs = (nb + 1) / 2;
     const unsigned grid = (unsigned)npairs * HKV * GG;
-    const size_t lds = kBufs * kTileFloats * sizeof(float);  // > 64 KB: opt in once per instantiation
+    const size_t lds = (size_t)kKS * kGroupF * sizeof(float);  // > 64 KB: opt in once per instantiation
+    static_assert(kKS * kGroupF >= 2 * 4 * kXchF * 64, "merge exchange must fit in the tile buffers");
     static bool opted[3] = {false, false, false};
     const int oi = GW == 1 ? 0 : GW == 2 ? 1 : 2;
     if (!opted[oi]) {
@@ -257,9 +285,9 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
         opted[oi] = true;
     }
     switch (GW) {
-        case 1: k_prefill<1><<<grid, 64, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale); break;
-        case 2: k_prefill<2><<<grid, 128, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale); break;
-        case 4: k_prefill<4><<<grid, 256, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale); break;
+        case 1: k_prefill<1><<<grid, 64 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale); break;
+        case 2: k_prefill<2><<<grid, 128 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale); break;
+        case 4: k_prefill<4><<<grid, 256 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
