@@ -23,9 +23,11 @@
 //
 // K/V tiles (32 keys) reach LDS by LDS DMA (global_load_lds_dwordx4) straight from the
 // cache, two tiles ahead for K and one for V, per key group:
-//   K tile chunk-major  [32 chunks of 4 d][32 keys][4 floats]: the 32 lanes reading one
-//     d-chunk of 32 different keys touch 512 contiguous bytes (no bank conflicts);
-//   V tile row-major    [32 keys][128 floats].
+//   K tile row-major, rows padded to 132 floats: the 32 lanes reading one 16-byte d-chunk
+//     of 32 different keys hit 32 distinct bank quads; each row is one 32-lane DMA
+//     instruction (a contiguous 512-byte global read: LDS DMA of 16-byte pieces gathered
+//     from many rows runs ~3.5x slower per CU than contiguous DMA);
+//   V tile row-major    [32 keys][128 floats], two rows per 64-lane DMA instruction.
 // Rows past the causal end are clamped to the last visible row (valid memory, masked out).
 //
 // Softmax runs in the exp2 domain (scores x scale x log2 e, one FMA per score).  The
@@ -47,8 +49,10 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kQB = 32;                          // queries per wave (and per block)
 constexpr int kKT = 32;                          // keys per tile
-constexpr int kTileF = kKT * kHeadDim;           // floats in one K or V tile (16 KB)
-constexpr int kGroupF = 4 * kTileF;              // per key group: 2 K + 2 V tile buffers
+constexpr int kKS_F = kHeadDim + 4;             // padded K row (floats)
+constexpr int kKTileF = kKT * kKS_F;             // floats in one K tile
+constexpr int kVTileF = kKT * kHeadDim;          // floats in one V tile (16 KB)
+constexpr int kGroupF = 2 * kKTileF + 2 * kVTileF;  // per key group: 2 K + 2 V tile buffers
 constexpr int kKS = 2;                           // key groups per workgroup
 constexpr float kLazy = 8.f;                     // lazy-rescale threshold (log2 units)
 constexpr int kXchF = 34;                        // floats per lane exchanged by the merge
@@ -60,7 +64,7 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
                                                            const int* __restrict__ pos_dev, int B, int H, int HKV,
                                                            int GG, float scale) {
     constexpr int D = kHeadDim;
-    constexpr int DMA_PER_WAVE = 16 / GW;  // DMA instructions per wave per K (or V) tile
+    constexpr int DMA_PER_WAVE = 16 / GW;  // V DMA instructions per wave per tile (K: twice as many, 32 lanes each)
     extern __shared__ __align__(16) float smem[];
 
     const int L = blockIdx.x;
@@ -80,6 +84,7 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
     const float* vbase = vc + (size_t)kvh * D;
     const int nb = (B + kQB - 1) / kQB;
     float* gsm = smem + grp * kGroupF;  // this key group's buffers: K0 K1 V0 V1
+    float* gsv = gsm + 2 * kKTileF;
     const float sl2 = scale * 1.44269504088896340736f;
 
     for (int pass = 0; pass < 2; ++pass) {
@@ -121,18 +126,19 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         // DMA of this group's i-th tile (kt = KS*i + grp) into a K or V buffer
         auto dma_k = [&](int i, int buf) {
             const int t0 = (kKS * i + grp) * kKT;
-            const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsm + buf * kTileF));
+            const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsm + buf * kKTileF));
+            if (hh == 0) {
 #pragma unroll
-            for (int j = 0; j < DMA_PER_WAVE; ++j) {
-                const int ins = hw * DMA_PER_WAVE + j;  // 1 KB = d-chunks 2*ins, 2*ins+1
-                const int chunk = 2 * ins + hh;
-                const int key = min(t0 + col, T - 1);
-                dma16(kbase + (size_t)key * KD + 4 * chunk, lb + ins * 1024);
+                for (int j = 0; j < 2 * DMA_PER_WAVE; ++j) {
+                    const int row = hw * 2 * DMA_PER_WAVE + j;  // one padded row per instruction
+                    const int key = min(t0 + row, T - 1);
+                    dma16(kbase + (size_t)key * KD + 4 * col, lb + row * (kKS_F * 4));
+                }
             }
         };
         auto dma_v = [&](int i, int buf) {
             const int t0 = (kKS * i + grp) * kKT;
-            const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsm + (2 + buf) * kTileF));
+            const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsv + buf * kVTileF));
 #pragma unroll
             for (int j = 0; j < DMA_PER_WAVE; ++j) {
                 const int ins = hw * DMA_PER_WAVE + j;  // 1 KB = keys 2*ins, 2*ins+1
@@ -141,16 +147,16 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
             }
         };
 
-        // S^T = K . Q^T for the K tile at Kt (chunk-major); the operand of step k4+1 is
+        // S^T = K . Q^T for the K tile at Kt (padded rows); the operand of step k4+1 is
         // read while the four MFMAs of step k4 run
         auto qk = [&](const float* Kt, floatx16& acc) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-            const float* kp = Kt + hh * 16 * (kKT * 4) + col * 4;
+            const float* kp = Kt + col * kKS_F + hh * 64;
             float4 kv = *reinterpret_cast<const float4*>(kp);
 #pragma unroll
             for (int k4 = 0; k4 < 16; ++k4) {
-                const float4 kn = *reinterpret_cast<const float4*>(kp + ((k4 + 1) & 15) * (kKT * 4));
+                const float4 kn = *reinterpret_cast<const float4*>(kp + 4 * ((k4 + 1) & 15));
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * k4 + 0], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qreg[4 * k4 + 1], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qreg[4 * k4 + 2], acc, 0, 0, 0);
@@ -160,7 +166,10 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         };
 
         // One tile kt of this group: softmax of its scores s (in place: s becomes P^T) and
-        // O^T += V^T . P^T with V at Vt; when Kn is set the next tile's scores go to sn.
+        // O^T += V^T . P^T with V at Vt, while the scores of the K tile at Kn go to sn.  The
+        // group's last tile passes the other (stale) K buffer as Kn and discards sn: a straight-line
+        // body keeps O in 64 VGPRs (a branch around either product makes the compiler
+        // split O across register files and spill at two waves per SIMD).
         auto step = [&](floatx16& s, floatx16& sn, int kt, const float* Kn, const float* Vt) {
             if (kt >= nfull) {  // tile crosses the diagonal (wave-uniform)
                 const int k0 = kt * kKT + 4 * hh;
@@ -183,20 +192,42 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
                 m = mn;
             }
             const float nb_ = m == -INFINITY ? 0.f : -m;
-            if (Kn) qk(Kn, sn);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 s[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], sl2, nb_));
                 lsum += s[r];
             }
+            // the next tile's score chain (64 dependent MFMAs) interleaved with this tile's
+            // P.V (four independent chains): one wave keeps the matrix pipe busy without
+            // waiting on its own accumulator
             const float* vp = Vt + 4 * hh * D + 4 * col;
+            auto vrow = [&](int r) {
+                return *reinterpret_cast<const float4*>(vp + (8 * (r >> 2) + (r & 3)) * D);
+            };
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sn[i] = 0.f;
+            const float* kp = Kn + col * kKS_F + hh * 64;
+            float4 kv = *reinterpret_cast<const float4*>(kp);
+            float4 vv = vrow(0);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float4 vv = *reinterpret_cast<const float4*>(vp + (8 * (r >> 2) + (r & 3)) * D);
+                const float4 kn = *reinterpret_cast<const float4*>(kp + 4 * ((r + 1) & 15));
+                const float4 vn = vrow((r + 1) & 15);
+                __builtin_amdgcn_sched_barrier(0);  // step r+1's operands are read before step r's MFMAs
+                sn = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * r + 0], sn, 0, 0, 0);
                 o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, s[r], o[0], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                sn = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qreg[4 * r + 1], sn, 0, 0, 0);
                 o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, s[r], o[1], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                sn = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qreg[4 * r + 2], sn, 0, 0, 0);
                 o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, s[r], o[2], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                sn = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qreg[4 * r + 3], sn, 0, 0, 0);
                 o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, s[r], o[3], 0, 0, 0);
+                kv = kn;
+                vv = vn;
+                __builtin_amdgcn_sched_barrier(0);  // prefetch distance stays one step (register budget)
             }
         };
 
@@ -218,8 +249,7 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
             if (i + 2 < n_mine) dma_k(i + 2, i & 1);
             if (i + 1 < n_mine) dma_v(i + 1, (i + 1) & 1);
             if (i < n_mine)
-                step(s, sn, kKS * i + grp, i + 1 < n_mine ? gsm + ((i + 1) & 1) * kTileF : nullptr,
-                     gsm + (2 + (i & 1)) * kTileF);
+                step(s, sn, kKS * i + grp, gsm + ((i + 1) & 1) * kKTileF, gsv + (i & 1) * kVTileF);
             wait_vmcnt<0>();
             __syncthreads();
         };
