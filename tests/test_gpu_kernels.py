@@ -88,12 +88,13 @@ def test_kv_append_bit_exact_and_untouched(orc, gpu, rows, pos0):
     assert bits_equal(kh, ref_k) and bits_equal(vh, ref_v)
 
 
-def test_qkv_prepare_matches_oracle(orc, gpu):
-    H, HKV, B, pos0 = 16, 8, 9, 30
+@pytest.mark.parametrize("H,HKV,B,pos0", [(16, 8, 9, 30), (4, 2, 16, 32), (8, 1, 3, 60)])
+def test_qkv_prepare_matches_oracle(orc, gpu, H, HKV, B, pos0):
     shape = gpu.AttnShape(H, HKV)
     qkv = orc.normal((B, shape.qkv), 21)
     qg, kg = orc.gamma(D, 1), orc.gamma(D, 2)
     n_ctx = 64
+    assert pos0 + B <= n_ctx
     cs = gpu.rope_table(n_ctx)
     kc = _dev(np.zeros((n_ctx, HKV * D), np.float32))
     vc = _dev(np.zeros((n_ctx, HKV * D), np.float32))
@@ -119,7 +120,8 @@ def _cache(orc, n, HKV, seed, spike_every=0):
 
 
 @pytest.mark.parametrize("H,HKV,T", [(16, 8, 1), (16, 8, 2), (32, 8, 63), (32, 8, 64), (32, 8, 65), (16, 8, 1000),
-                                     (32, 8, 4096), (8, 8, 333), (64, 8, 700)])
+                                     (32, 8, 4096), (8, 8, 333), (64, 8, 700), (4, 2, 64), (8, 2, 300),
+                                     (16, 4, 129), (4, 1, 77), (8, 1, 2048)])
 def test_decode_matches_reference_attention(orc, gpu, H, HKV, T):
     shape = gpu.AttnShape(H, HKV)
     k, v = _cache(orc, T + 5, HKV, 40 + T)
@@ -174,7 +176,7 @@ def test_decode_batched_ragged(orc, gpu):
     assert rel_err(out, ref) <= ATTN_RTOL
 
 
-@pytest.mark.parametrize("H,HKV,T", [(32, 8, 1), (32, 8, 4096), (16, 8, 777)])
+@pytest.mark.parametrize("H,HKV,T", [(32, 8, 1), (32, 8, 4096), (16, 8, 777), (4, 2, 55), (8, 1, 300)])
 def test_fused_decode_step(orc, gpu, H, HKV, T):
     """ei_decode_step == headnorm_rope(Q,K) + append + reference attention, bit-exact cache."""
     shape = gpu.AttnShape(H, HKV)
@@ -199,7 +201,9 @@ def test_fused_decode_step(orc, gpu, H, HKV, T):
 
 # ---------------------------------------------------------------- prefill
 @pytest.mark.parametrize("H,HKV,B,pos0", [(16, 8, 1, 0), (16, 8, 31, 0), (32, 8, 33, 0), (16, 8, 100, 37),
-                                          (32, 8, 512, 0), (16, 8, 512, 512), (32, 8, 65, 1000), (64, 8, 40, 3)])
+                                          (32, 8, 512, 0), (16, 8, 512, 512), (32, 8, 65, 1000), (64, 8, 40, 3),
+                                          (4, 2, 16, 32), (8, 2, 48, 0), (16, 4, 70, 5), (4, 4, 20, 3),
+                                          (8, 1, 97, 200)])
 def test_prefill_matches_reference_attention(orc, gpu, H, HKV, B, pos0):
     shape = gpu.AttnShape(H, HKV)
     n = pos0 + B

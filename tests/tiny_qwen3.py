@@ -1,0 +1,134 @@
+"""A tiny random-weight Qwen3 forward pass in numpy: the end-to-end harness for the attention path.
+
+Test infrastructure only.  No Qwen3 GGUF exists in this environment, so the end-to-end gate
+(|delta logprob| <= 2.7e-5 between the reference's attention and this build's) is measured on a
+synthetic model with the Qwen3 block structure of src/model.cpp:157-236:
+
+    h   = rmsnorm(x) * attn_norm                       (src/model.cpp:167)
+    qkv = h @ [Wq; Wk; Wv]^T                            (:170-172)
+    per-head QK-norm + RoPE, KV append, attention       (:174-214)  <- the path under test
+    x  += att @ Wo^T                                    (:216)
+    h   = rmsnorm(x) * ffn_norm; x += (silu(h Wg^T) * (h Wu^T)) Wd^T   (:218-230)
+    logits = rmsnorm(x) * out_norm @ Wlm^T              (:233-236)
+
+Everything except the attention callback is shared numpy float32 code, so two runs differ only
+by how the attention sub-step (norm, RoPE, append, softmax attention) is computed.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+HEAD_DIM = 128
+
+
+def _rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    ss = np.sum(x.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    inv = (1.0 / np.sqrt(ss / x.shape[-1] + eps)).astype(np.float32)
+    return (x * inv) * w
+
+
+def _silu(x: np.ndarray) -> np.ndarray:
+    return x / (1.0 + np.exp(-x))
+
+
+class TinyQwen3:
+    """Random Qwen3-shaped weights (head_dim 128); fan-in scaled so activations stay O(1)."""
+
+    def __init__(self, seed: int, n_layer: int = 2, n_embd: int = 256, n_head: int = 4, n_head_kv: int = 2,
+                 n_ff: int = 512, n_vocab: int = 384):
+        rng = np.random.default_rng(seed)
+        D = HEAD_DIM
+        self.n_layer, self.E, self.H, self.HKV, self.V = n_layer, n_embd, n_head, n_head_kv, n_vocab
+
+        def mat(rows, cols, gain=1.0):
+            return (rng.standard_normal((rows, cols)) * (gain / np.sqrt(cols))).astype(np.float32)
+
+        def norm_w(n):
+            return (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+
+        self.emb = rng.standard_normal((n_vocab, n_embd)).astype(np.float32)
+        self.layers = []
+        for _ in range(n_layer):
+            self.layers.append(dict(
+                attn_norm=norm_w(n_embd),
+                wqkv=mat((n_head + 2 * n_head_kv) * D, n_embd),
+                q_norm=norm_w(D), k_norm=norm_w(D),
+                wo=mat(n_embd, n_head * D),
+                ffn_norm=norm_w(n_embd),
+                wg=mat(n_ff, n_embd), wu=mat(n_ff, n_embd), wd=mat(n_embd, n_ff),
+            ))
+        self.out_norm = norm_w(n_embd)
+        self.lm = mat(n_vocab, n_embd, gain=2.0)
+
+    @property
+    def qkv_width(self) -> int:
+        return (self.H + 2 * self.HKV) * HEAD_DIM
+
+    def forward(self, tokens: np.ndarray, pos0: int, attn) -> np.ndarray:
+        """Logits [n, vocab] for tokens at positions pos0.. ; attn(l, qkv [n, qkv_width], pos0) -> [n, H*128]."""
+        x = self.emb[tokens]
+        for l, L in enumerate(self.layers):
+            h = _rmsnorm(x, L["attn_norm"])
+            qkv = np.ascontiguousarray(h @ L["wqkv"].T, dtype=np.float32)
+            att = attn(l, qkv, pos0)
+            x = x + att @ L["wo"].T
+            h = _rmsnorm(x, L["ffn_norm"])
+            x = x + (_silu(h @ L["wg"].T) * (h @ L["wu"].T)) @ L["wd"].T
+        return _rmsnorm(x, self.out_norm) @ self.lm.T
+
+
+def logprobs(logits: np.ndarray, targets: np.ndarray) -> np.ndarray:
+    """log softmax(logits)[target] per row, evaluated in float64 from the float32 logits."""
+    z = logits.astype(np.float64)
+    z = z - z.max(axis=-1, keepdims=True)
+    lse = np.log(np.exp(z).sum(axis=-1))
+    return z[np.arange(len(targets)), targets] - lse
+
+
+def run_sequence(model: TinyQwen3, attn_factory, tokens: np.ndarray, chunks: list[int], n_decode: int,
+                 n_ctx: int) -> np.ndarray:
+    """Prompt in `chunks` (prefill), then `n_decode` greedy-free decode steps on the given tokens.
+
+    `tokens` holds sum(chunks) + n_decode + 1 ids; the logprob of token i+1 is scored at every
+    position i.  attn_factory(n_ctx) returns the attention callback with its own KV cache.
+    """
+    attn = attn_factory(n_ctx)
+    out = []
+    pos = 0
+    for n in chunks:
+        lg = model.forward(tokens[pos:pos + n], pos, attn)
+        out.append(logprobs(lg, tokens[pos + 1:pos + n + 1]))
+        pos += n
+    for _ in range(n_decode):
+        lg = model.forward(tokens[pos:pos + 1], pos, attn)
+        out.append(logprobs(lg, tokens[pos + 1:pos + 2]))
+        pos += 1
+    return np.concatenate(out)
+
+
+def oracle_attention(model: TinyQwen3, O, scale: float | None = None, f64: bool = False):
+    """Attention callback built on the CPU restatement (oracle/oracle.py) with per-layer caches."""
+    D, H, HKV = HEAD_DIM, model.H, model.HKV
+
+    def factory(n_ctx: int):
+        kc = [np.zeros((n_ctx, HKV * D), np.float32) for _ in range(model.n_layer)]
+        vc = [np.zeros((n_ctx, HKV * D), np.float32) for _ in range(model.n_layer)]
+
+        def attn(l, qkv, pos0):
+            L = model.layers[l]
+            buf = O.headnorm_rope(qkv, H, D, L["q_norm"], pos0, D, 1e6, 1e-6)  # returns a normed copy
+            buf = O.headnorm_rope(buf, HKV, D, L["k_norm"], pos0, D, 1e6, 1e-6, col0=H * D)
+            O.kv_append(buf[:, H * D:(H + HKV) * D], buf[:, (H + HKV) * D:], kc[l], vc[l], pos0)
+            n = buf.shape[0]
+            q = np.ascontiguousarray(buf[:, :H * D])
+            if f64:
+                rows = [O.attn_f64(q[b].reshape(H, D), kc[l], vc[l], pos0 + b + 1, H, HKV, D, scale)
+                        for b in range(n)]
+                return np.stack(rows).reshape(n, H * D).astype(np.float32)
+            if n == 1:
+                return O.attn_decode(q.reshape(H, D), kc[l], vc[l], pos0 + 1, H, HKV, D, scale).reshape(1, H * D)
+            return O.attn_prefill(q, kc[l], vc[l], n, pos0, H, HKV, D, scale).reshape(n, H * D)
+
+        return attn
+
+    return factory
