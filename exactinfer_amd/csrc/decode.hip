@@ -20,7 +20,9 @@
 //             (2 rows x G heads) and a transposing butterfly over lanes xor 1/2/4 leaves
 //             one finished score per lane (7 exchanges for G = 4).
 //   softmax   the tile max per head is a 4-step butterfly over the lanes holding that
-//             head; p = exp(s - m) goes to a wave-private LDS row.
+//             head; p = 2^(s*scale*log2(e) - m) (one v_exp_f32) goes to a wave-private
+//             LDS row.  The K rows of a tile are waited for first: scores and softmax
+//             overlap the transfer of its V rows.
 //   values    lane l owns d = 2l, 2l+1 of all 16 rows and accumulates p * v for the G
 //             heads.
 //
@@ -243,23 +245,23 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
 #pragma unroll
     for (int k = 0; k < NF; ++k) l[k] = 0.f;
     const int sidx = xreduce8_index<NV>(c);
+    const float sl2 = a.scale * 1.44269504088896340736f;  // scores in log2 units: p = 2^(s - m)
 
     int slot_i = 0;
     for (int t0 = tw0; t0 < t_end; t0 += kStride, slot_i = (slot_i + 1) % kRing) {
-        if (kRing == 2 && t0 + kStride < t_end) wait_vmcnt<kTile>();  // this tile landed; the next may fly
-        else wait_vmcnt<0>();
+        // this tile's K rows have landed (its 8 V instructions and the next tile may still
+        // fly): the scores and softmax overlap the V transfer
+        const bool next_flying = kRing == 2 && t0 + kStride < t_end;
+        if (next_flying) wait_vmcnt<kTile + kTile / 2>();
+        else wait_vmcnt<kTile / 2>();
         float* tk = wring + slot_i * kTileFloats;
         float* tv = tk + kTile * D;
-
-        if constexpr (FUSED) {
-            const int kr = pos - t0;
-            if (owner && kr >= 0 && kr < kTile) {  // the new row: overwrite what the DMA brought
-                *reinterpret_cast<float2*>(tk + tile_off(kr, lane >> 1) + 2 * (lane & 1)) =
-                    *reinterpret_cast<const float2*>(&knew[0][2 * lane]);
-                *reinterpret_cast<float2*>(tv + tile_off(kr, lane >> 1) + 2 * (lane & 1)) =
-                    *reinterpret_cast<const float2*>(&knew[1][2 * lane]);
-                __builtin_amdgcn_wave_barrier();
-            }
+        const int kr = pos - t0;  // fused: row of the new key in this tile, if any
+        const bool patch = FUSED && owner && kr >= 0 && kr < kTile;
+        if (patch) {  // the new row: overwrite what the DMA brought
+            *reinterpret_cast<float2*>(tk + tile_off(kr, lane >> 1) + 2 * (lane & 1)) =
+                *reinterpret_cast<const float2*>(&knew[0][2 * lane]);
+            __builtin_amdgcn_wave_barrier();
         }
 
         // ---- scores: partial dots, 8-lane transposing reduction
@@ -280,7 +282,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
 #pragma unroll
         for (int k = 0; k < NF; ++k) {
             const int idx = sidx + k, j = idx / G, g = idx % G;
-            const float sv = t0 + 8 * j + r < t_end ? part[k] * a.scale : -INFINITY;
+            const float sv = t0 + 8 * j + r < t_end ? part[k] * sl2 : -INFINITY;
             float mt = fmaxf(sv, lane_xor1(sv));  // lanes holding this head: xor 1, 8, 16, 32
             mt = fmaxf(mt, lane_xor8(mt));
             mt = fmaxf(mt, lane_xor16(mt));
@@ -289,8 +291,8 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
 #pragma unroll
             for (int gg = 1; gg < G; ++gg) mold = g == gg ? m[gg] : mold;
             const float mn = fmaxf(mold, mt);  // finite: the tile holds at least one visible key
-            const float p = expf(sv - mn);
-            l[k] = l[k] * expf(mold - mn) + p;
+            const float p = __builtin_amdgcn_exp2f(sv - mn);
+            l[k] = l[k] * __builtin_amdgcn_exp2f(mold - mn) + p;
             pw[w][(8 * j + r) * G + g] = p;
             if (r == 0 && j == 0) mw[w][g] = mn;
         }
@@ -298,12 +300,19 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float mn = mw[w][g];
-            const float corr = expf(m[g] - mn);
+            const float corr = __builtin_amdgcn_exp2f(m[g] - mn);
             m[g] = mn;
             acc[g].x *= corr;
             acc[g].y *= corr;
         }
-        // ---- values: acc[g][d] += p[row][g] * V[row][d]
+        // ---- values: acc[g][d] += p[row][g] * V[row][d], once the V rows have landed
+        if (next_flying) wait_vmcnt<kTile>();
+        else wait_vmcnt<0>();
+        if (patch) {
+            *reinterpret_cast<float2*>(tv + tile_off(kr, lane >> 1) + 2 * (lane & 1)) =
+                *reinterpret_cast<const float2*>(&knew[1][2 * lane]);
+            __builtin_amdgcn_wave_barrier();
+        }
         const int voff = 2 * (lane & 1);
 #pragma unroll
         for (int k = 0; k < kTile; ++k) {
@@ -358,7 +367,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
 #pragma unroll
         for (int ww = 0; ww < kWaves; ++ww) {
             if (mws[ww] == -INFINITY) continue;
-            const float wv = expf(mws[ww] - Mw);
+            const float wv = __builtin_amdgcn_exp2f(mws[ww] - Mw);
             Lw = fmaf(wv, wml[ww][G + gcol], Lw);
             const float4 v = *reinterpret_cast<const float4*>(&wacc[ww * G * D + gcol * D + 4 * d4]);
             o.x = fmaf(wv, v.x, o.x);
@@ -388,7 +397,8 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
 }
 
 // Split combine as a separate launch: grid (n_seq * H), 128 threads (thread = d).  All
-// (m, l) and accumulator loads of the S splits are issued before any is used.
+// (m, l) and accumulator loads of the S splits are issued before any is used.  m is in
+// log2 units (the decode kernel's exp2 domain).
 template <int G>
 __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
     constexpr int D = kHeadDim;
@@ -425,7 +435,7 @@ __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
 #pragma unroll
                 for (int k = 0; k < kDecodeMaxSplits / 64; ++k) {
                     const int s = tid + 64 * k;
-                    const float wv = mv[k] == -INFINITY ? 0.f : expf(mv[k] - M);  // empty split: skipped
+                    const float wv = mv[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv[k] - M);  // empty split: skipped
                     if (s < S) wsh[s] = wv;
                     L = fmaf(wv, lv[k], L);
                 }
