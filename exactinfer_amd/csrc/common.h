@@ -71,10 +71,24 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v + lane_xor32(v);
 }
 
+// Butterfly sum of a double over the wave: both halves of the double move through the same
+// DPP / swizzle exchanges as the float helpers (no LDS round trips).  Partners add the same
+// two values, so every lane ends with identical bits.
+template <int M>
+__device__ __forceinline__ double lane_xor_f64(double v) {
+    const unsigned long long b = __double_as_longlong(v);
+    const float lo = lane_xor<M>(__uint_as_float((unsigned)b));
+    const float hi = lane_xor<M>(__uint_as_float((unsigned)(b >> 32)));
+    return __longlong_as_double((long long)(((unsigned long long)__float_as_uint(hi) << 32) | __float_as_uint(lo)));
+}
+
 __device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
-    return v;
+    v += lane_xor_f64<1>(v);
+    v += lane_xor_f64<2>(v);
+    v += lane_xor_f64<4>(v);
+    v += lane_xor_f64<8>(v);
+    v += lane_xor_f64<16>(v);
+    return v + lane_xor_f64<32>(v);
 }
 
 // ------------------------------------------------------------------ LDS DMA
