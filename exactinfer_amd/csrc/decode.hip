@@ -146,6 +146,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     constexpr int NV = 2 * G;                     // partial dots per lane in the score phase
     constexpr int NF = NV / 8 > 0 ? NV / 8 : 1;   // finished scores per lane after xreduce8
     constexpr int NCOL = G * 32;                  // float4 columns of the G output heads
+    static_assert(kRing * kTileFloats >= G * kHeadDim, "a wave's ring slots hold its partial");
     extern __shared__ __align__(16) float ring[];          // [kWaves][kRing][kTileFloats]; later scratch
     __shared__ __align__(16) float qs[G * D];
     __shared__ __align__(16) float pw[kWaves][kTile * G];  // per wave: p[row][g] of the current tile
@@ -344,10 +345,10 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
             wml[w][G + g] = lv;
         }
     }
-    __syncthreads();  // every wave is past its key loop: the ring can hold the wave partials
-    float* wacc = ring;  // [kWaves][G*D]
+    // the wave's accumulator goes to its own ring slot: private to the wave, and every DMA
+    // into it has landed (the key loop ends with a full wait), so one barrier suffices
 #pragma unroll
-    for (int g = 0; g < G; ++g) *reinterpret_cast<float2*>(&wacc[w * G * D + g * D + 2 * lane]) = acc[g];
+    for (int g = 0; g < G; ++g) *reinterpret_cast<float2*>(&wring[g * D + 2 * lane]) = acc[g];
     __syncthreads();
 
     // thread t < NCOL merges float4 column (g, d4)
@@ -369,7 +370,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
             if (mws[ww] == -INFINITY) continue;
             const float wv = __builtin_amdgcn_exp2f(mws[ww] - Mw);
             Lw = fmaf(wv, wml[ww][G + gcol], Lw);
-            const float4 v = *reinterpret_cast<const float4*>(&wacc[ww * G * D + gcol * D + 4 * d4]);
+            const float4 v = *reinterpret_cast<const float4*>(&ring[ww * (kRing * kTileFloats) + gcol * D + 4 * d4]);
             o.x = fmaf(wv, v.x, o.x);
             o.y = fmaf(wv, v.y, o.y);
             o.z = fmaf(wv, v.z, o.z);
