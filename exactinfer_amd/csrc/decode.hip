@@ -113,7 +113,7 @@ __device__ __forceinline__ int tile_off(int row, int chunk) {
 }
 
 // Issue the 16 DMA instructions of one tile: K rows t0..t0+15 then V rows (two rows per
-// instruction).  Rows past t_end are clamped to the last visible row (valid memory; their
+// instruction), non-temporal: each byte of the cache is read once per step.  Rows past t_end are clamped to the last visible row (valid memory; their
 // scores are masked out).
 __device__ __forceinline__ void issue_tile(const float* slot, const float* kbase, const float* vbase, size_t KD,
                                            int t0, int t_end, int lane) {
@@ -124,14 +124,14 @@ __device__ __forceinline__ void issue_tile(const float* slot, const float* kbase
         const int row = 2 * t + half;
         const int key = min(t0 + row, t_end - 1);
         const int chunk = s ^ ((row & 1) << 3);
-        dma16(kbase + (size_t)key * KD + 4 * chunk, base + t * 1024);
+        dma16_nt(kbase + (size_t)key * KD + 4 * chunk, base + t * 1024);
     }
 #pragma unroll
     for (int t = 0; t < kTile / 2; ++t) {
         const int row = 2 * t + half;
         const int key = min(t0 + row, t_end - 1);
         const int chunk = s ^ ((row & 1) << 3);
-        dma16(vbase + (size_t)key * KD + 4 * chunk, base + kTile * kHeadDim * 4 + t * 1024);
+        dma16_nt(vbase + (size_t)key * KD + 4 * chunk, base + kTile * kHeadDim * 4 + t * 1024);
     }
 }
 
