@@ -102,13 +102,32 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // see a pending LDS write and serialise unrelated LDS accesses behind it; completion is
 // tracked by hand with wait_vmcnt (each instruction counts one in vmcnt).
 __device__ __forceinline__ void dma16(const float* g, uint32_t m0_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0_base) : "memory", "m0");
+    // m0_base is wave-uniform by construction; readfirstlane keeps it in an SGPR even when
+    // the compiler computed it in VGPRs (e.g. inside a divergent branch)
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
+                 "s"(__builtin_amdgcn_readfirstlane(m0_base))
+                 : "memory", "m0");
 }
 
 // The same with the non-temporal (streaming) cache policy, for data read once: a decode
 // step's KV stream runs ~11% faster with it than with the default policy on MI355X.
 __device__ __forceinline__ void dma16_nt(const float* g, uint32_t m0_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "s"(m0_base) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g),
+                 "s"(__builtin_amdgcn_readfirstlane(m0_base))
+                 : "memory", "m0");
+}
+
+// Scalar-base form: lane address = sbase (wave-uniform 64-bit byte address in SGPRs) +
+// voff (32-bit per-lane byte offset).  With per-lane offsets fixed for a whole loop, each
+// instruction costs only scalar arithmetic for its base.
+__device__ __forceinline__ void dma16_s(uint64_t sbase, uint32_t voff, uint32_t m0_base) {
+    // the operands are uniform by construction; readfirstlane states it to the compiler
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)sbase);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(sbase >> 32));
+    const uint64_t sb = ((uint64_t)hi << 32) | lo;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb),
+                 "s"(__builtin_amdgcn_readfirstlane(m0_base))
+                 : "memory", "m0");
 }
 
 // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at 15:14,

@@ -82,6 +82,10 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
     const size_t KD = (size_t)HKV * D;
     const float* kbase = kc + (size_t)kvh * D;
     const float* vbase = vc + (size_t)kvh * D;
+    const uint64_t kb_bytes = (uint64_t)(uintptr_t)kbase, vb_bytes = (uint64_t)(uintptr_t)vbase;
+    const uint32_t row_bytes = (uint32_t)(KD * sizeof(float));          // one cache row (all KV heads)
+    const uint32_t voff_k = 16u * col;                                  // K: lanes 0..31, one row
+    const uint32_t voff_v = (uint32_t)hh * row_bytes + 16u * col;        // V: two rows per instruction
     const int nb = (B + kQB - 1) / kQB;
     float* gsm = smem + grp * kGroupF;  // this key group's buffers: K0 K1 V0 V1
     float* gsv = gsm + 2 * kKTileF;
@@ -124,26 +128,43 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         const int n_mine = (ntile - grp + kKS - 1) / kKS;  // tiles of this key group
 
         // DMA of this group's i-th tile (kt = KS*i + grp) into a K or V buffer
+        // DMA of this group's i-th tile (kt = KS*i + grp).  A tile wholly below T uses the
+        // scalar-base form with per-lane byte offsets fixed for the pass; the tile that
+        // reaches past T clamps each row to the last visible one (valid memory, masked out).
         auto dma_k = [&](int i, int buf) {
             const int t0 = (kKS * i + grp) * kKT;
             const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsm + buf * kKTileF));
+            const int r0 = hw * 2 * DMA_PER_WAVE;  // this wave's first row of the tile
             if (hh == 0) {
+                if (t0 + kKT <= T) {
+                    const uint64_t sb = kb_bytes + (uint64_t)(uint32_t)(t0 + r0) * row_bytes;
 #pragma unroll
-                for (int j = 0; j < 2 * DMA_PER_WAVE; ++j) {
-                    const int row = hw * 2 * DMA_PER_WAVE + j;  // one padded row per instruction
-                    const int key = min(t0 + row, T - 1);
-                    dma16(kbase + (size_t)key * KD + 4 * col, lb + row * (kKS_F * 4));
+                    for (int j = 0; j < 2 * DMA_PER_WAVE; ++j)  // one padded row per instruction
+                        dma16_s(sb + (uint64_t)j * row_bytes, voff_k, lb + (r0 + j) * (kKS_F * 4));
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 2 * DMA_PER_WAVE; ++j) {
+                        const int key = min(t0 + r0 + j, T - 1);
+                        dma16(kbase + (size_t)key * KD + 4 * col, lb + (r0 + j) * (kKS_F * 4));
+                    }
                 }
             }
         };
         auto dma_v = [&](int i, int buf) {
             const int t0 = (kKS * i + grp) * kKT;
             const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsv + buf * kVTileF));
+            const int i0 = hw * DMA_PER_WAVE;  // 1 KB instruction = keys 2*ins, 2*ins+1
+            if (t0 + kKT <= T) {
+                const uint64_t sb = vb_bytes + (uint64_t)(uint32_t)(t0 + 2 * i0) * row_bytes;
 #pragma unroll
-            for (int j = 0; j < DMA_PER_WAVE; ++j) {
-                const int ins = hw * DMA_PER_WAVE + j;  // 1 KB = keys 2*ins, 2*ins+1
-                const int key = min(t0 + 2 * ins + hh, T - 1);
-                dma16(vbase + (size_t)key * KD + 4 * col, lb + ins * 1024);
+                for (int j = 0; j < DMA_PER_WAVE; ++j)
+                    dma16_s(sb + (uint64_t)(2 * j) * row_bytes, voff_v, lb + (i0 + j) * 1024);
+            } else {
+#pragma unroll
+                for (int j = 0; j < DMA_PER_WAVE; ++j) {
+                    const int key = min(t0 + 2 * (i0 + j) + hh, T - 1);
+                    dma16(vbase + (size_t)key * KD + 4 * col, lb + (i0 + j) * 1024);
+                }
             }
         };
 
