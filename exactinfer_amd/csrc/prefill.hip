@@ -10,8 +10,9 @@
 // exchange with lane^32.  The same registers, unchanged, are the B operand of
 //     O^T[d][query] = V^T . P^T          (A = V from LDS)
 // because the accumulator row order (8*(r/4) + 4*(lane/32) + r%4) is used as the
-// contraction order of the second product.  The contraction order over d in the first
-// product is (lane/32)*64 + step, so each lane's Q^T operand is 64 contiguous floats.
+// contraction order of the second product.  In the first product, step 4*k4 + j of lane
+// half hh contracts d = 8*k4 + 4*hh + j: the two halves of a wave read neighbouring 16-byte
+// pieces of each query row, so one q load instruction touches 32 cache lines, not 64.
 // Output block db (0..3) of O^T holds d = 4*i + db for accumulator row i, so the A operand
 // of all four blocks for one key is a single 16-byte LDS read V[key][4*lane .. 4*lane+3].
 //
@@ -97,13 +98,13 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         const int b = qb * kQB + col;  // this lane's query row
         const int qpos = pos0 + b;
 
-        // Q^T operand: q[b][h][hh*64 + kk], kk < 64
+        // Q^T operand: qreg[4*k4 + j] = q[b][h][8*k4 + 4*hh + j]
         float qreg[64];
         if (b < B) {
-            const float* src = q + (size_t)b * q_stride + (size_t)h * D + hh * 64;
+            const float* src = q + (size_t)b * q_stride + (size_t)h * D + 4 * hh;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float4 v = *reinterpret_cast<const float4*>(src + 4 * i);
+                const float4 v = *reinterpret_cast<const float4*>(src + 8 * i);
                 qreg[4 * i] = v.x;
                 qreg[4 * i + 1] = v.y;
                 qreg[4 * i + 2] = v.z;
@@ -173,11 +174,11 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         auto qk = [&](const float* Kt, floatx16& acc) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-            const float* kp = Kt + col * kKS_F + hh * 64;
+            const float* kp = Kt + col * kKS_F + 4 * hh;  // K[key col][8*k4 + 4*hh ..]
             float4 kv = *reinterpret_cast<const float4*>(kp);
 #pragma unroll
             for (int k4 = 0; k4 < 16; ++k4) {
-                const float4 kn = *reinterpret_cast<const float4*>(kp + 4 * ((k4 + 1) & 15));
+                const float4 kn = *reinterpret_cast<const float4*>(kp + 8 * ((k4 + 1) & 15));
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * k4 + 0], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qreg[4 * k4 + 1], acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qreg[4 * k4 + 2], acc, 0, 0, 0);
@@ -227,12 +228,12 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
             };
 #pragma unroll
             for (int i = 0; i < 16; ++i) sn[i] = 0.f;
-            const float* kp = Kn + col * kKS_F + hh * 64;
+            const float* kp = Kn + col * kKS_F + 4 * hh;
             float4 kv = *reinterpret_cast<const float4*>(kp);
             float4 vv = vrow(0);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float4 kn = *reinterpret_cast<const float4*>(kp + 4 * ((r + 1) & 15));
+                const float4 kn = *reinterpret_cast<const float4*>(kp + 8 * ((r + 1) & 15));
                 const float4 vn = vrow((r + 1) & 15);
                 __builtin_amdgcn_sched_barrier(0);  // step r+1's operands are read before step r's MFMAs
                 sn = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * r + 0], sn, 0, 0, 0);
