@@ -92,14 +92,10 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
     float* gsv = gsm + 2 * kKTileF;
     const float sl2 = scale * 1.44269504088896340736f;
 
-    for (int pass = 0; pass < 2; ++pass) {
-        const int qb = pass == 0 ? pair : nb - 1 - pair;
-        if (pass == 1 && qb == pair) break;
-        const int b = qb * kQB + col;  // this lane's query row
-        const int qpos = pos0 + b;
-
-        // Q^T operand: qreg[4*k4 + j] = q[b][h][8*k4 + 4*hh + j]
-        float qreg[64];
+    // Q^T operand of query block qb: qreg[4*k4 + j] = q[qb*32 + col][h][8*k4 + 4*hh + j]
+    float qreg[64];
+    auto load_q = [&](int qb) {
+        const int b = qb * kQB + col;
         if (b < B) {
             const float* src = q + (size_t)b * q_stride + (size_t)h * D + 4 * hh;
 #pragma unroll
@@ -114,6 +110,15 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
 #pragma unroll
             for (int i = 0; i < 64; ++i) qreg[i] = 0.f;
         }
+    };
+    const int qb_second = nb - 1 - pair;  // the pass-1 block (none when it equals pair)
+    load_q(pair);
+
+    for (int pass = 0; pass < 2; ++pass) {
+        const int qb = pass == 0 ? pair : qb_second;
+        if (pass == 1 && qb == pair) break;
+        const int b = qb * kQB + col;  // this lane's query row
+        const int qpos = pos0 + b;
 
         floatx16 o[4];
 #pragma unroll
@@ -279,6 +284,9 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
             iter(i, sa, sb);
             if (i + 1 < n_it) iter(i + 1, sb, sa);
         }
+
+        // the next block's q loads fly during the merge (qreg is dead after the key loop)
+        if (pass == 0 && qb_second != pair) load_q(qb_second);
 
         // ---- merge the key groups through LDS (tile buffers are free after the barrier):
         // group g finalises output blocks db = 2g, 2g+1 and hands the other two to its partner
