@@ -138,25 +138,34 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // ------------------------------------------------------------------ QK-norm + RoPE of one head
-// One wave normalises and rotates one 128-float head vector.
+// One wave normalises and rotates one 128-float head vector; lane l holds elements l
+// (x0) and l+64 (x1).
 //   ss  = sum of double(x)^2 (tree order; the value in double matches the sequential
 //         sum to ~1e-16 relative, so the float `inv` is the reference's except within an
 //         ulp-rounding tie)                                   src/ops.cpp:155-160
 //   inv = float(1 / sqrt(ss/128 + double(eps)));  y = (x * inv) * gamma
 //   NEOX rotation of halves with the table's (cos, sin):      src/model.cpp:23-32
 //   y[i] = a*c - b*s,  y[i+half] = a*s + b*c   (no FMA contraction: two products, then +/-)
-// `dst` is LDS scratch of 128 floats owned by this wave (may alias nothing else).
-// Returns in *o0 / *o1 the outputs for elements lane and lane+64.
-__device__ __forceinline__ void norm_rope_head(const float* __restrict__ src, const float* __restrict__ gamma,
+// With rope_dim = 128 (Qwen3) the partners i and i+64 sit in the same lane and the rotation
+// is done in registers; other rope_dims exchange partners through `dst`, 128 floats of
+// LDS scratch owned by this wave.  Returns the outputs for elements lane and lane+64.
+__device__ __forceinline__ void norm_rope_vals(float x0, float x1, float g0, float g1,
                                                const float2* __restrict__ cs_row, int rope_dim, float eps,
                                                float* dst, int lane, float* o0, float* o1) {
 #pragma clang fp contract(off)
-    const float x0 = src[lane], x1 = src[lane + 64];
     double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
     ss = wave_sum_f64(ss);
     const float inv = (float)(1.0 / sqrt(ss / (double)kHeadDim + (double)eps));
-    const float y0 = (x0 * inv) * gamma[lane];
-    const float y1 = (x1 * inv) * gamma[lane + 64];
+    const float y0 = (x0 * inv) * g0;
+    const float y1 = (x1 * inv) * g1;
+    if (rope_dim == kHeadDim) {
+        const float2 t = cs_row[lane];
+        const float acs = y0 * t.x, bsn = y1 * t.y;
+        const float asn = y0 * t.y, bcs = y1 * t.x;
+        *o0 = acs - bsn;
+        *o1 = asn + bcs;
+        return;
+    }
     dst[lane] = y0;
     dst[lane + 64] = y1;
     __builtin_amdgcn_wave_barrier();
@@ -186,6 +195,13 @@ __device__ __forceinline__ void norm_rope_head(const float* __restrict__ src, co
     __builtin_amdgcn_wave_barrier();
     *o0 = r0;
     *o1 = r1;
+}
+
+__device__ __forceinline__ void norm_rope_head(const float* __restrict__ src, const float* __restrict__ gamma,
+                                               const float2* __restrict__ cs_row, int rope_dim, float eps,
+                                               float* dst, int lane, float* o0, float* o1) {
+    norm_rope_vals(src[lane], src[lane + 64], gamma[lane], gamma[lane + 64], cs_row, rope_dim, eps, dst, lane, o0,
+                   o1);
 }
 
 // ------------------------------------------------------------------ synthetic inputs

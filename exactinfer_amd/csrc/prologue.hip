@@ -40,9 +40,12 @@ __global__ __launch_bounds__(256) void k_kv_append(const float* __restrict__ k_s
     }
 }
 
-// grid (rows, ceil((H+HKV)/4)), block 256.  Head index hh < H: query head (q_gamma);
-// otherwise key head hh-H (k_gamma), whose normed row also goes to the cache together
-// with the raw V row of the same kv head.  src/cuda/model_cuda.cu:1800-1806.
+// grid (rows, ceil((H+HKV)/16)), block 256: each wave takes 4 consecutive heads of the
+// row (2 KB) and issues all their loads (and the V rows of its key heads) before any
+// arithmetic, so a wave keeps 8-16 loads in flight.  Head index hh < H: query head
+// (q_gamma); otherwise key head hh-H (k_gamma), whose normed row also goes to the cache
+// together with the raw V row of the same kv head.  src/cuda/model_cuda.cu:1800-1806.
+constexpr int kPrepHeads = 4;  // heads per wave
 __global__ __launch_bounds__(256) void k_qkv_prepare(float* __restrict__ qkv, long row_stride, int H, int HKV,
                                                      const float* __restrict__ q_gamma,
                                                      const float* __restrict__ k_gamma,
@@ -51,27 +54,46 @@ __global__ __launch_bounds__(256) void k_qkv_prepare(float* __restrict__ qkv, lo
                                                      float* __restrict__ vc) {
     __shared__ float scratch[4][kHeadDim];
     const int b = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int hh = blockIdx.y * 4 + w;
-    if (hh >= H + HKV) return;
+    const int NH = H + HKV;
+    const int h0 = (blockIdx.y * 4 + w) * kPrepHeads;
+    if (h0 >= NH) return;  // wave-uniform; this kernel has no block barrier
     float* row = qkv + (size_t)b * row_stride;
-    float* v = row + (size_t)hh * kHeadDim;
     const int pos = *pos_dev + b;
-    const bool is_k = hh >= H;
-    float o0, o1;
-    norm_rope_head(v, is_k ? k_gamma : q_gamma, cs + (size_t)pos * (rope_dim >> 1), rope_dim, eps, scratch[w], lane,
-                   &o0, &o1);
-    v[lane] = o0;
-    v[lane + 64] = o1;
-    if (is_k) {
-        const int kvh = hh - H;
-        const size_t kd = (size_t)HKV * kHeadDim;
-        float* kd_row = kc + (size_t)pos * kd + (size_t)kvh * kHeadDim;
-        float* vd_row = vc + (size_t)pos * kd + (size_t)kvh * kHeadDim;
-        const float* vs = row + (size_t)(H + HKV) * kHeadDim + (size_t)kvh * kHeadDim;
-        kd_row[lane] = o0;
-        kd_row[lane + 64] = o1;
-        vd_row[lane] = vs[lane];
-        vd_row[lane + 64] = vs[lane + 64];
+    const float2* cs_row = cs + (size_t)pos * (rope_dim >> 1);
+    float x0[kPrepHeads], x1[kPrepHeads], v0[kPrepHeads], v1[kPrepHeads];
+#pragma unroll
+    for (int j = 0; j < kPrepHeads; ++j) {
+        const int hh = min(h0 + j, NH - 1);  // clamped: heads past NH are loaded, not used
+        const float* v = row + (size_t)hh * kHeadDim;
+        x0[j] = v[lane];
+        x1[j] = v[lane + 64];
+        const float* vs = row + (size_t)(H + HKV + max(hh - H, 0)) * kHeadDim;  // V of a key head
+        v0[j] = vs[lane];
+        v1[j] = vs[lane + 64];
+    }
+    const float qg0 = q_gamma[lane], qg1 = q_gamma[lane + 64];
+    const float kg0 = k_gamma[lane], kg1 = k_gamma[lane + 64];
+    const size_t kd = (size_t)HKV * kHeadDim;
+#pragma unroll
+    for (int j = 0; j < kPrepHeads; ++j) {
+        const int hh = h0 + j;
+        if (hh >= NH) break;
+        const bool is_k = hh >= H;
+        float o0, o1;
+        norm_rope_vals(x0[j], x1[j], is_k ? kg0 : qg0, is_k ? kg1 : qg1, cs_row, rope_dim, eps, scratch[w], lane,
+                       &o0, &o1);
+        float* v = row + (size_t)hh * kHeadDim;
+        v[lane] = o0;
+        v[lane + 64] = o1;
+        if (is_k) {
+            const int kvh = hh - H;
+            float* kd_row = kc + (size_t)pos * kd + (size_t)kvh * kHeadDim;
+            float* vd_row = vc + (size_t)pos * kd + (size_t)kvh * kHeadDim;
+            kd_row[lane] = o0;
+            kd_row[lane + 64] = o1;
+            vd_row[lane] = v0[j];
+            vd_row[lane + 64] = v1[j];
+        }
     }
 }
 
@@ -104,7 +126,8 @@ hipError_t launch_kv_append(hipStream_t st, const float* k_src, const float* v_s
 hipError_t launch_qkv_prepare(hipStream_t st, float* qkv, int rows, long row_stride, int H, int HKV,
                               const float* q_gamma, const float* k_gamma, const float* cs, const int* pos_dev,
                               int rope_dim, float eps, float* kc, float* vc) {
-    k_qkv_prepare<<<dim3(rows, (H + HKV + 3) / 4), 256, 0, st>>>(qkv, row_stride, H, HKV, q_gamma, k_gamma,
+    const int groups = (H + HKV + 4 * kPrepHeads - 1) / (4 * kPrepHeads);  // 4 waves x kPrepHeads heads
+    k_qkv_prepare<<<dim3(rows, groups), 256, 0, st>>>(qkv, row_stride, H, HKV, q_gamma, k_gamma,
                                                                   reinterpret_cast<const float2*>(cs), pos_dev,
                                                                   rope_dim, eps, kc, vc);
     return hipGetLastError();
