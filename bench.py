@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch the per-layer kernels eagerly")
     ap.add_argument("--extra", action="store_true", help="also measure configs[3] and configs[4]")
-    ap.add_argument("--only", choices=["decode", "prefill", "longctx", "batched"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill-chunked", "longctx", "batched"], default=None)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
     return ap.parse_args()
@@ -253,6 +253,31 @@ def bench_prefill(torch, A, H, HKV, n_layer, T, steps, warmup, seed=2000):
             "kernel_tflops": flops_layer / (kern_ms * 1e-3) / 1e12, "flops_per_launch": flops_layer}
 
 
+def bench_prefill_chunked(torch, A, H, HKV, n_layer, T, chunk, split=True, seed=2100):
+    """configs[2]'s prompt as the reference engine feeds it: chunks of `chunk` tokens at pos0 = 0, chunk, ...
+    (src/cuda/model_cuda.cu:1912 caps a prefill chunk at 512).  Attention launches only, one graph."""
+    shape = A.AttnShape(H, HKV)
+    dev = "cuda"
+    kd = HKV * D
+    q = A.synth_fill(torch.empty((n_layer, T, shape.qkv), dtype=torch.float32, device=dev), seed)
+    kc = A.synth_fill(torch.empty((n_layer, T, kd), dtype=torch.float32, device=dev), seed + 1)
+    vc = A.synth_fill(torch.empty((n_layer, T, kd), dtype=torch.float32, device=dev), seed + 2)
+    out = torch.empty((n_layer, T, H, D), dtype=torch.float32, device=dev)
+    starts = list(range(0, T, chunk))
+    pos = [torch.tensor([s], dtype=torch.int32, device=dev) for s in starts]
+    ws = A.PrefillWorkspace(chunk, H, HKV, T) if split else None  # the engine's path: key split for short chunks
+
+    def run():
+        for l in range(n_layer):
+            for s, p in zip(starts, pos):
+                n = min(chunk, T - s)
+                A.attn_prefill(q[l, s:s + n], kc[l], vc[l], p, shape, B=n, out=out[l, s:s + n], ws=ws)
+
+    ms = graph_ms(torch, run, reps=5, warm=1) / n_layer
+    flops = A.flops_causal(T, 0, H)
+    return {"chunk": chunk, "key_split": split, "kernel_ms_per_layer": ms, "kernel_tflops": flops / (ms * 1e-3) / 1e12}
+
+
 # ---------------------------------------------------------------- CPU baseline
 def cpu_baseline(budget_s: float = 12.0):
     """Reference CPU attention loop (oracle restatement of src/model.cpp:191-214, OpenMP over
@@ -307,6 +332,11 @@ def main():
         log("prefill configs[2] ...")
         res["prefill"] = bench_prefill(torch, A, 32, 8, 36, 2048, args.prefill_steps, 1)
         log(json.dumps(res["prefill"]))
+    if args.extra or args.only == "prefill-chunked":
+        log("prefill configs[2] in 512-token chunks ...")
+        res["prefill_chunked"] = bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512)
+        log(json.dumps(res["prefill_chunked"]))
+        log(json.dumps(bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512, split=False)))
     if args.extra or args.only == "longctx":
         log("long-context decode configs[3] ...")
         res["longctx"] = bench_decode(torch, A, 16, 8, 28, 32768, max(8, args.steps // 8), 3, use_graph,

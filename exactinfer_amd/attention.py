@@ -162,15 +162,34 @@ def decode_step(qkv: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, shape: At
 
 
 # ---------------------------------------------------------------- prefill
+class PrefillWorkspace:
+    """Key-split shares for ei_attn_prefill_split: serves chunks of up to max_B rows with
+    pos0 + B <= max_kv (max_kv only steers the split plan; larger positions stay correct)."""
+
+    def __init__(self, max_B: int, n_head: int, n_head_kv: int, max_kv: int, device="cuda"):
+        self.max_B, self.max_kv = max_B, max_kv
+        self.nbytes = int(_capi.lib().ei_attn_prefill_ws_bytes(max_B, n_head, n_head_kv, max_kv))
+        self.buf = torch.empty(max(self.nbytes, 256), dtype=torch.uint8, device=device)
+
+
 def attn_prefill(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos_dev: torch.Tensor, shape: AttnShape,
-                 B: int | None = None, scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """q rows [B, >= H*128] (normed + roped, heads first); returns [B, H, 128]."""
+                 B: int | None = None, scale: float | None = None, out: torch.Tensor | None = None,
+                 ws: PrefillWorkspace | None = None) -> torch.Tensor:
+    """q rows [B, >= H*128] (normed + roped, heads first); returns [B, H, 128].
+    With `ws` the key range is split over workgroups for short chunks (ei_attn_prefill_split)."""
     _need_gpu_f32("q", q)
     B = q.shape[0] if B is None else B
     out = torch.empty((B, shape.n_head, HEAD_DIM), dtype=torch.float32, device=q.device) if out is None else out
     scale = default_scale() if scale is None else scale
-    _capi.call("ei_attn_prefill", _stream(), q.data_ptr(), q.stride(0), out.data_ptr(), kc.data_ptr(),
-               vc.data_ptr(), pos_dev.data_ptr(), B, shape.n_head, shape.n_head_kv, shape.head_dim, float(scale))
+    if ws is None:
+        _capi.call("ei_attn_prefill", _stream(), q.data_ptr(), q.stride(0), out.data_ptr(), kc.data_ptr(),
+                   vc.data_ptr(), pos_dev.data_ptr(), B, shape.n_head, shape.n_head_kv, shape.head_dim, float(scale))
+    else:
+        if B > ws.max_B:
+            raise ValueError(f"prefill workspace serves chunks of up to {ws.max_B} rows, got B={B}")
+        _capi.call("ei_attn_prefill_split", _stream(), q.data_ptr(), q.stride(0), out.data_ptr(), kc.data_ptr(),
+                   vc.data_ptr(), pos_dev.data_ptr(), B, shape.n_head, shape.n_head_kv, shape.head_dim, float(scale),
+                   ws.max_kv, ws.buf.data_ptr(), ws.nbytes)
     return out
 
 

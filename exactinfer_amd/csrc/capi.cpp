@@ -246,7 +246,36 @@ EI_API int ei_attn_prefill(ei_stream_t stream, const float* q, long q_stride, fl
     REQUIRE(aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc), "pointers must be 16-byte aligned");
     if (B == 0) return ok();
     return hip_status(ei::launch_prefill(static_cast<hipStream_t>(stream), q, q_stride, out, kc, vc, pos_dev, B,
-                                         n_head, n_head_kv, scale),
+                                         n_head, n_head_kv, scale, 1, nullptr),
+                      "prefill launch");
+}
+
+EI_API size_t ei_attn_prefill_ws_bytes(int max_B, int n_head, int n_head_kv, int max_kv) {
+    if (max_B <= 0 || n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv || max_kv < max_B) return 0;
+    size_t most = 0;  // the plan varies with B: size for every chunk of up to max_B rows
+    for (int b = 1; b <= max_B; ++b) {
+        const size_t need = ei::prefill_ws_bytes(b, n_head, n_head_kv, max_kv);
+        if (need > most) most = need;
+    }
+    return most;
+}
+
+EI_API int ei_attn_prefill_split(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc,
+                                 const float* vc, const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim,
+                                 float scale, int max_kv, void* ws, size_t ws_bytes) {
+    if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
+    REQUIRE(q && out && kc && vc && pos_dev, "null pointer argument");
+    REQUIRE(B >= 0, "B %d", B);
+    REQUIRE(max_kv >= B, "max_kv %d < B %d", max_kv, B);
+    REQUIRE(q_stride >= (long)n_head * head_dim && q_stride % 4 == 0, "q_stride %ld", q_stride);
+    REQUIRE(aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc), "pointers must be 16-byte aligned");
+    if (B == 0) return ok();
+    const int ksplit = ei::prefill_split(B, n_head, n_head_kv, max_kv);
+    const size_t need = ei::prefill_ws_bytes(B, n_head, n_head_kv, max_kv);
+    REQUIRE(ws_bytes >= need, "workspace %zu B < %zu B (ei_attn_prefill_ws_bytes)", ws_bytes, need);
+    REQUIRE(need == 0 || (ws && aligned16(ws)), "workspace must be a 16-byte aligned device pointer");
+    return hip_status(ei::launch_prefill(static_cast<hipStream_t>(stream), q, q_stride, out, kc, vc, pos_dev, B,
+                                         n_head, n_head_kv, scale, ksplit, ws),
                       "prefill launch");
 }
 

@@ -56,7 +56,13 @@ hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fu
 hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes);
 
 // ------------------------------------------------------------------ prefill.hip
+// Key split across workgroups for short chunks: ksplit shares per query block, merged by a
+// second launch; fixed by (B, max_kv) so graphs replay unchanged.
+constexpr int kPrefillMaxSplit = 8;
+int prefill_split(int B, int H, int HKV, int max_kv);
+size_t prefill_ws_bytes(int B, int H, int HKV, int max_kv);  // 0 when no split is planned
 hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
-                          const float* vc, const int* pos_dev, int B, int H, int HKV, float scale);
+                          const float* vc, const int* pos_dev, int B, int H, int HKV, float scale, int ksplit,
+                          void* ws);
 
 }  // namespace ei

@@ -63,7 +63,8 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
                                                            float* __restrict__ out, const float* __restrict__ kc,
                                                            const float* __restrict__ vc,
                                                            const int* __restrict__ pos_dev, int B, int H, int HKV,
-                                                           int GG, float scale) {
+                                                           int GG, float scale, int ksplit,
+                                                           float* __restrict__ part_o, float* __restrict__ part_ml) {
     constexpr int D = kHeadDim;
     constexpr int DMA_PER_WAVE = 16 / GW;  // V DMA instructions per wave per tile (K: twice as many, 32 lanes each)
     extern __shared__ __align__(16) float smem[];
@@ -72,7 +73,8 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
     const int kvh = L % HKV;
     const int rest = L / HKV;
     const int hg = rest % GG;
-    const int pair = rest / GG;
+    const int split = (rest / GG) % ksplit;  // which contiguous share of each block's key tiles
+    const int pair = (rest / GG) / ksplit;
     const int G = GW * GG;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wu = __builtin_amdgcn_readfirstlane(w);  // wave-uniform: keeps the branches scalar
@@ -130,15 +132,17 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         const int T = pos0 + min(B, qb * kQB + kQB);   // keys seen by the block's last query
         const int ntile = (T + kKT - 1) / kKT;
         const int nfull = (pos0 + qb * kQB + 1) / kKT;  // tiles below the diagonal (no mask)
-        const int n_it = (ntile + kKS - 1) / kKS;
-        const int n_mine = (ntile - grp + kKS - 1) / kKS;  // tiles of this key group
+        const int kt_lo = split * ntile / ksplit;       // this workgroup's tiles: [kt_lo, kt_hi)
+        const int nrange = (split + 1) * ntile / ksplit - kt_lo;
+        const int n_it = (nrange + kKS - 1) / kKS;
+        const int n_mine = (nrange - grp + kKS - 1) / kKS;  // tiles of this key group
 
         // DMA of this group's i-th tile (kt = KS*i + grp) into a K or V buffer
         // DMA of this group's i-th tile (kt = KS*i + grp).  A tile wholly below T uses the
         // scalar-base form with per-lane byte offsets fixed for the pass; the tile that
         // reaches past T clamps each row to the last visible one (valid memory, masked out).
         auto dma_k = [&](int i, int buf) {
-            const int t0 = (kKS * i + grp) * kKT;
+            const int t0 = (kt_lo + kKS * i + grp) * kKT;
             const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsm + buf * kKTileF));
             const int r0 = hw * 2 * DMA_PER_WAVE;  // this wave's first row of the tile
             if (hh == 0) {
@@ -157,7 +161,7 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
             }
         };
         auto dma_v = [&](int i, int buf) {
-            const int t0 = (kKS * i + grp) * kKT;
+            const int t0 = (kt_lo + kKS * i + grp) * kKT;
             const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsv + buf * kVTileF));
             const int i0 = hw * DMA_PER_WAVE;  // 1 KB instruction = keys 2*ins, 2*ins+1
             if (t0 + kKT <= T) {
@@ -276,7 +280,7 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
             if (i + 2 < n_mine) dma_k(i + 2, i & 1);
             if (i + 1 < n_mine) dma_v(i + 1, (i + 1) & 1);
             if (i < n_mine)
-                step(s, sn, kKS * i + grp, gsm + ((i + 1) & 1) * kKTileF, gsv + (i & 1) * kVTileF);
+                step(s, sn, kt_lo + kKS * i + grp, gsm + ((i + 1) & 1) * kKTileF, gsv + (i & 1) * kVTileF);
             wait_vmcnt<0>();
             __syncthreads();
         };
@@ -304,32 +308,119 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         __syncthreads();
         const float* xp = smem + ((1 - grp) * GW + hw) * (kXchF * 64) + lane;
         const float mp = xp[0], lp = xp[64];
-        const float mt = fmaxf(m, mp);  // finite: key 0 is visible to every lane
-        const float c0 = __builtin_amdgcn_exp2f(m - mt), cp = __builtin_amdgcn_exp2f(mp - mt);
+        const float mt = fmaxf(m, mp);  // -inf only when this share holds no visible key for the query
+        const float c0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mt);
+        const float cp = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - mt);
         const float l = half_sum(lsum * c0 + lp * cp);
-        const float inv = 1.f / l;
         if (b < B) {
             // O^T register r of block db is d = 4*(8(r/4) + 4hh + r%4) + db
-            float* dst = out + ((size_t)b * H + h) * D + 16 * hh + 2 * grp;
+            const size_t rowh = (size_t)b * H + h;
+            if (ksplit == 1) {
+                const float inv = 1.f / l;
+                float* dst = out + rowh * D + 16 * hh + 2 * grp;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float2 v;
-                v.x = (keep0[r] * c0 + xp[(2 + r) * 64] * cp) * inv;
-                v.y = (keep1[r] * c0 + xp[(18 + r) * 64] * cp) * inv;
-                *reinterpret_cast<float2*>(dst + 4 * (8 * (r >> 2) + (r & 3))) = v;
+                for (int r = 0; r < 16; ++r) {
+                    float2 v;
+                    v.x = (keep0[r] * c0 + xp[(2 + r) * 64] * cp) * inv;
+                    v.y = (keep1[r] * c0 + xp[(18 + r) * 64] * cp) * inv;
+                    *reinterpret_cast<float2*>(dst + 4 * (8 * (r >> 2) + (r & 3))) = v;
+                }
+            } else {
+                // unnormalised share (m in log2 units, l, O) for k_prefill_combine
+                const size_t slot = (size_t)split * B * H + rowh;
+                float* dst = part_o + slot * D + 16 * hh + 2 * grp;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float2 v;
+                    v.x = keep0[r] * c0 + xp[(2 + r) * 64] * cp;
+                    v.y = keep1[r] * c0 + xp[(18 + r) * 64] * cp;
+                    *reinterpret_cast<float2*>(dst + 4 * (8 * (r >> 2) + (r & 3))) = v;
+                }
+                if (hh == 0 && grp == 0) *reinterpret_cast<float2*>(part_ml + slot * 2) = make_float2(mt, l);
             }
         }
     }
 }
 
+// Merge of the ksplit shares of every (query, head): grid ceil(B*H/4), 128 threads; thread
+// = float4 column d4 of row (b, h).  o = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, empty
+// shares (m = -inf) skipped.
+__global__ __launch_bounds__(128) void k_prefill_combine(const float* __restrict__ part_o,
+                                                         const float* __restrict__ part_ml, float* __restrict__ out,
+                                                         int rows, int ksplit) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 5), d4 = threadIdx.x & 31;
+    if (row >= rows) return;
+    float M = -INFINITY;
+    for (int s = 0; s < ksplit; ++s) M = fmaxf(M, part_ml[((size_t)s * rows + row) * 2]);
+    float L = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < ksplit; ++s) {
+        const size_t slot = (size_t)s * rows + row;
+        const float2 ml = *reinterpret_cast<const float2*>(part_ml + slot * 2);
+        if (ml.x == -INFINITY) continue;
+        const float wv = __builtin_amdgcn_exp2f(ml.x - M);
+        const float4 v = *reinterpret_cast<const float4*>(part_o + slot * kHeadDim + 4 * d4);
+        L = fmaf(wv, ml.y, L);
+        o.x = fmaf(wv, v.x, o.x);
+        o.y = fmaf(wv, v.y, o.y);
+        o.z = fmaf(wv, v.z, o.z);
+        o.w = fmaf(wv, v.w, o.w);
+    }
+    const float inv = 1.f / L;
+    o.x *= inv;
+    o.y *= inv;
+    o.z *= inv;
+    o.w *= inv;
+    *reinterpret_cast<float4*>(out + (size_t)row * kHeadDim + 4 * d4) = o;
+}
+
+static int prefill_grid1(int B, int H, int HKV) {
+    const int G = H / HKV;
+    const int GG = G / (G < 4 ? G : 4);
+    const int nb = (B + kQB - 1) / kQB;
+    return ((nb + 1) / 2) * HKV * GG;
+}
+
+int prefill_split(int B, int H, int HKV, int max_kv) {
+    // One workgroup per (query-block pair, KV head) fills the chip only for long chunks.  A
+    // chunk with fewer workgroups than CUs splits every block's key tiles into ksplit
+    // contiguous shares, as many as bring the grid to about one workgroup per CU while
+    // each share keeps >= 4 tiles on average (max_kv bounds pos0 + B on the host, which
+    // does not see the device-resident position).
+    const int g1 = prefill_grid1(B, H, HKV);
+    if (g1 >= 256) return 1;
+    const long avg_tiles = ((long)max_kv - B / 2 + kKT - 1) / kKT;
+    int k = (256 + g1 - 1) / g1;
+    const long cap = avg_tiles / 4 > 1 ? avg_tiles / 4 : 1;
+    if (k > cap) k = (int)cap;
+    if (k > kPrefillMaxSplit) k = kPrefillMaxSplit;
+    return k < 1 ? 1 : k;
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t prefill_ws_bytes(int B, int H, int HKV, int max_kv) {
+    const int k = prefill_split(B, H, HKV, max_kv);
+    if (k <= 1) return 0;
+    const size_t rows = (size_t)B * H;
+    return align256((size_t)k * rows * kHeadDim * sizeof(float)) + align256((size_t)k * rows * 2 * sizeof(float));
+}
+
 hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
-                          const float* vc, const int* pos_dev, int B, int H, int HKV, float scale) {
+                          const float* vc, const int* pos_dev, int B, int H, int HKV, float scale, int ksplit,
+                          void* ws) {
     const int G = H / HKV;
     const int GW = G < 4 ? G : 4;
     const int GG = G / GW;
-    const int nb = (B + kQB - 1) / kQB;
-    const int npairs = (nb + 1) / 2;
-    const unsigned grid = (unsigned)npairs * HKV * GG;
+    if (ksplit < 1) ksplit = 1;
+    const unsigned grid = (unsigned)prefill_grid1(B, H, HKV) * ksplit;
+    float* part_o = nullptr;
+    float* part_ml = nullptr;
+    if (ksplit > 1) {
+        const size_t rows = (size_t)B * H;
+        part_o = static_cast<float*>(ws);
+        part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256((size_t)ksplit * rows * kHeadDim * 4));
+    }
     const size_t lds = (size_t)kKS * kGroupF * sizeof(float);  // > 64 KB: opt in once per instantiation
     static_assert(kKS * kGroupF >= 2 * 4 * kXchF * 64, "merge exchange must fit in the tile buffers");
     static bool opted[3] = {false, false, false};
@@ -345,10 +436,23 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
         opted[oi] = true;
     }
     switch (GW) {
-        case 1: k_prefill<1><<<grid, 64 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale); break;
-        case 2: k_prefill<2><<<grid, 128 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale); break;
-        case 4: k_prefill<4><<<grid, 256 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale); break;
+        case 1:
+            k_prefill<1><<<grid, 64 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale, ksplit,
+                                                      part_o, part_ml);
+            break;
+        case 2:
+            k_prefill<2><<<grid, 128 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale,
+                                                       ksplit, part_o, part_ml);
+            break;
+        case 4:
+            k_prefill<4><<<grid, 256 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale,
+                                                       ksplit, part_o, part_ml);
+            break;
         default: return hipErrorInvalidValue;
+    }
+    if (ksplit > 1) {
+        const int rows = B * H;
+        k_prefill_combine<<<(rows + 3) / 4, 128, 0, st>>>(part_o, part_ml, out, rows, ksplit);
     }
     return hipGetLastError();
 }

@@ -46,6 +46,9 @@ HipAttention::HipAttention(const AttnConfig& cfg, int n_ctx, int max_batch, hipS
     hip_check(hipMalloc(&ws_, ws_bytes_), "decode workspace");
     check(ei_attn_workspace_init(stream_, ws_, ws_bytes_));
 
+    pws_bytes_ = ei_attn_prefill_ws_bytes(max_batch_ < n_ctx_ ? max_batch_ : n_ctx_, c_.n_head, c_.n_head_kv, n_ctx_);
+    if (pws_bytes_) hip_check(hipMalloc(&pws_, pws_bytes_), "prefill workspace");
+
     hip_check(hipMalloc(&pos_dev_, sizeof(int)), "position");
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&pos_host_), sizeof(int), hipHostMallocDefault), "pinned position");
     hip_check(hipStreamSynchronize(stream_), "init");
@@ -56,6 +59,7 @@ HipAttention::~HipAttention() {
     if (pos_host_) (void)hipHostFree(pos_host_);
     if (pos_dev_) (void)hipFree(pos_dev_);
     if (ws_) (void)hipFree(ws_);
+    if (pws_) (void)hipFree(pws_);
     if (rope_) (void)hipFree(rope_);
     if (kv_) (void)hipFree(kv_);
 }
@@ -94,7 +98,8 @@ void HipAttention::layer(int l, float* qkv, long qkv_stride, const float* q_norm
         // cache rows 0..pos0+b (earlier chunks included)
         check(ei_qkv_prepare(stream_, qkv, B_, qkv_stride, H, HKV, D, q_norm, k_norm, rope_, pos_dev_, c_.rope_dim,
                              c_.eps, kcache(l), vcache(l)));
-        check(ei_attn_prefill(stream_, qkv, qkv_stride, att, kcache(l), vcache(l), pos_dev_, B_, H, HKV, D, scale_));
+        check(ei_attn_prefill_split(stream_, qkv, qkv_stride, att, kcache(l), vcache(l), pos_dev_, B_, H, HKV, D,
+                                    scale_, n_ctx_, pws_, pws_bytes_));
     }
 }
 

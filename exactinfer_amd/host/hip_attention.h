@@ -54,7 +54,8 @@ public:
     //   q_norm / k_norm: the layer's attn_q_norm / attn_k_norm weights [128] (device);
     //   att [B][H*128] output (device).
     // B == 1 runs the fused decode step (qkv is read only); B > 1 normalises Q and K in place,
-    // appends the chunk's K/V and runs the causal fp32-MFMA prefill.
+    // appends the chunk's K/V and runs the causal fp32-MFMA prefill (key range split over
+    // workgroups when the chunk alone would not fill the GPU).
     void layer(int l, float* qkv, long qkv_stride, const float* q_norm, const float* k_norm, float* att);
 
     // Device views of layer l's cache, [n_ctx][n_head_kv][128] fp32.
@@ -70,8 +71,10 @@ private:
     int B_ = 0;
     float* kv_ = nullptr;    // K caches of all layers, then V caches
     float* rope_ = nullptr;  // [n_ctx][rope_dim/2][2]
-    void* ws_ = nullptr;
+    void* ws_ = nullptr;  // decode split partials
     size_t ws_bytes_ = 0;
+    void* pws_ = nullptr;  // prefill key-split shares (chunks of up to max_batch rows)
+    size_t pws_bytes_ = 0;
     int* pos_dev_ = nullptr;
     int* pos_host_ = nullptr;  // pinned
     float scale_;

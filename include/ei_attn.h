@@ -126,6 +126,20 @@ int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride, float*
 int ei_attn_prefill(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc, const float* vc,
                     const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim, float scale);
 
+/* Key-split prefill for short chunks at long positions.  The reference engine feeds a prompt
+ * in chunks of at most 512 tokens (src/cuda/model_cuda.cu:1912) and runs one
+ * k_attn_prefill64 per chunk; at 512 tokens one workgroup per query-block pair and KV head
+ * leaves most CUs idle.  This variant splits every query block's key range over up to 8
+ * workgroups (planned from B and max_kv, an upper bound of *pos_dev + B) and merges the
+ * shares with a second launch, using `ws`: ei_attn_prefill_ws_bytes(max_B, ...) bytes serve
+ * every chunk of up to max_B rows (0 bytes when no split is planned; the call then equals
+ * ei_attn_prefill).  Same semantics and arguments as ei_attn_prefill otherwise; no
+ * counterpart in the reference beyond k_attn_prefill64.  Calls sharing `ws` must not overlap. */
+size_t ei_attn_prefill_ws_bytes(int max_B, int n_head, int n_head_kv, int max_kv);
+int ei_attn_prefill_split(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc,
+                          const float* vc, const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim,
+                          float scale, int max_kv, void* ws, size_t ws_bytes);
+
 /* ------------------------------------------------------------------ synthetic inputs
  * Not part of the reference path: fills n floats with the counter-based N(0,1)
  * generator (element e = stream element offset+e of `seed`), multiplying by spike_mult

@@ -64,3 +64,24 @@ def test_decode_workspace_size_is_monotone():
     c = L.ei_attn_decode_ws_bytes(64, 16, 8, 8192)
     assert 0 < a <= b and c > 0
     assert L.ei_attn_decode_ws_bytes(1, 30, 8, 10) == 0
+
+
+def test_prefill_split_workspace_contract():
+    from exactinfer_amd import _capi
+    L = _capi.lib()
+    # chunks of one row over one cache row never split: no workspace
+    assert L.ei_attn_prefill_ws_bytes(1, 32, 8, 1) == 0
+    # a 512-token chunk with up to 2048 cache rows splits its key range
+    a = L.ei_attn_prefill_ws_bytes(512, 32, 8, 2048)
+    assert a > 0
+    # the size serves every chunk of up to max_B rows, so it never shrinks as max_B grows
+    sizes = [L.ei_attn_prefill_ws_bytes(m, 32, 8, 4096) for m in (1, 32, 100, 256, 512, 1024)]
+    assert all(x <= y for x, y in zip(sizes, sizes[1:]))
+    assert L.ei_attn_prefill_ws_bytes(0, 32, 8, 2048) == 0
+    assert L.ei_attn_prefill_ws_bytes(512, 30, 8, 2048) == 0
+    assert L.ei_attn_prefill_ws_bytes(512, 32, 8, 100) == 0  # max_kv < max_B
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    with pytest.raises(_capi.EiError, match="workspace"):
+        _capi.call("ei_attn_prefill_split", None, p, 4096, p, p, p, p, 512, 32, 8, 128, 0.1, 2048, p, 16)
+    with pytest.raises(_capi.EiError, match="max_kv"):
+        _capi.call("ei_attn_prefill_split", None, p, 4096, p, p, p, p, 512, 32, 8, 128, 0.1, 100, p, 1 << 30)

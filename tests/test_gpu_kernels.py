@@ -298,3 +298,54 @@ def test_prefill_graph_replays(orc, gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert bits_equal(_host(out), eager)
+
+
+# ---------------------------------------------------------------- key-split prefill (short chunks, long positions)
+@pytest.mark.gpu
+@pytest.mark.parametrize("H,HKV,B,pos0,max_kv", [(32, 8, 512, 1536, 2048), (16, 8, 100, 3000, 4096),
+                                                 (8, 2, 64, 500, 1024), (32, 8, 33, 0, 4096),
+                                                 (4, 1, 256, 7000, 8192), (64, 8, 40, 900, 1024)])
+def test_prefill_split_matches_reference_attention(orc, gpu, H, HKV, B, pos0, max_kv):
+    """ei_attn_prefill_split == the reference per-token attention; (32, 8, 33, 0, 4096) plans
+    more shares than the chunk has tiles, so empty shares are merged too."""
+    shape = gpu.AttnShape(H, HKV)
+    n = pos0 + B
+    k, v = _cache(orc, n, HKV, 90 + B)
+    q = orc.normal((B, H * D), 91 + pos0)
+    ws = gpu.PrefillWorkspace(B, H, HKV, max_kv)
+    assert ws.nbytes > 0, "this shape should plan a key split"
+    out = _host(gpu.attn_prefill(_dev(q), _dev(k), _dev(v), _pos(pos0), shape, ws=ws))
+    ref = orc.attn_prefill(q, k, v, B, pos0, H, HKV, D)
+    exact = None
+    if rel_err(out, ref) > ATTN_RTOL:  # long rows: the reference's sequential fp32 sums drift
+        kk, vv = k.reshape(n, -1), v.reshape(n, -1)
+        exact = np.stack([orc.attn_f64(q[b].reshape(H, D), kk, vv, pos0 + b + 1, H, HKV, D) for b in range(B)])
+    ok, msg = attn_parity(out, ref, exact)
+    assert ok, msg
+
+
+@pytest.mark.gpu
+def test_prefill_split_graph_replays_track_position(orc, gpu):
+    """One captured split prefill replayed at three device positions (the plan is fixed by
+    (B, max_kv)); each replay equals the reference at that position."""
+    import torch
+    H, HKV, B, max_kv = 16, 8, 128, 2048
+    shape = gpu.AttnShape(H, HKV)
+    k, v = _cache(orc, max_kv, HKV, 1400)
+    qh = orc.normal((B, H * D), 1401)
+    q, kd, vd = _dev(qh), _dev(k), _dev(v)
+    pos = _pos(0)
+    ws = gpu.PrefillWorkspace(B, H, HKV, max_kv)
+    out = torch.empty((B, H, D), dtype=torch.float32, device="cuda")
+    gpu.attn_prefill(q, kd, vd, pos, shape, out=out, ws=ws)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gpu.attn_prefill(q, kd, vd, pos, shape, out=out, ws=ws)
+    for p0 in (0, 700, max_kv - B):
+        pos.fill_(p0)
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = orc.attn_prefill(qh, k, v, B, p0, H, HKV, D)
+        assert rel_err(_host(out), ref) <= ATTN_RTOL, f"pos0 {p0}"
