@@ -464,13 +464,15 @@ static int pow2_ceil(long x) {
 }
 
 DecodePlan decode_plan(int n_seq, int HKV, int max_kv) {
-    // Aim at about one workgroup per CU (256 CUs): chunk = keys per workgroup, a power of
-    // two in [128, 2048] (128 fills every wave's two-tile ring once); the split count
-    // stays within the combine's LDS table.
-    const long rows = (long)max_kv * n_seq * HKV;
-    int chunk = pow2_ceil((rows + 255) / 256);
+    // One workgroup per (sequence, KV head) streams the most bytes per launch and needs no
+    // combine; keys are split only as far as it takes to reach about one workgroup per CU
+    // (256): chunk = max_kv / ceil(256 / (n_seq * HKV)), rounded up to a power of two >= 128
+    // (128 fills every wave's two-tile ring once).  The split count stays within the
+    // combine's table.
+    const long units = (long)n_seq * HKV;
+    const long want = units >= 256 ? 1 : (256 + units - 1) / units;
+    int chunk = pow2_ceil(((long)max_kv + want - 1) / want);
     if (chunk < 128) chunk = 128;
-    if (chunk > 2048) chunk = 2048;
     if (const char* env = std::getenv("EI_DECODE_CHUNK")) {  // tuning override (multiple of 64)
         const int v = std::atoi(env);
         if (v >= 64 && v % 64 == 0) chunk = v;
