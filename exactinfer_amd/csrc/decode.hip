@@ -165,7 +165,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     float* vbase = a.vc + row0 * KD + (size_t)kvh * D;
     const int t_begin = split * a.chunk;
     const int t_end = min(len, t_begin + a.chunk);
-    const int pos = len - 1;
+    const int pos = len > 0 ? len - 1 : 0;  // a zero-length sequence has no new row; keep the table index valid
     const float* qrow = a.q + (size_t)seq * a.q_stride;
     const int h0 = kvh * G;
     float* wring = ring + w * (kRing * kTileFloats);
@@ -380,10 +380,12 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
 
     if (S == 1) {  // a single split is already the answer
         if (tid < NCOL) {
-            o.x /= Lw;
-            o.y /= Lw;
-            o.z /= Lw;
-            o.w /= Lw;
+            if (Lw > 0.f) {
+                o.x /= Lw;
+                o.y /= Lw;
+                o.z /= Lw;
+                o.w /= Lw;
+            }  // else no keys (kv_len 0): o is zeros
             *reinterpret_cast<float4*>(a.out + (size_t)seq * a.H * D + (size_t)(h0 + gcol) * D + 4 * d4) = o;
         }
         return;
@@ -449,7 +451,7 @@ __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
         for (int b = 0; b < B; ++b)
             if (s0 + b < S) acc = fmaf(wsh[s0 + b], v[b], acc);
     }
-    a.out[(size_t)seq * a.H * D + (size_t)hq * D + tid] = acc / Lsh;
+    a.out[(size_t)seq * a.H * D + (size_t)hq * D + tid] = Lsh > 0.f ? acc / Lsh : 0.f;  // kv_len 0: zeros
 }
 
 __global__ void k_ws_clear(uint32_t* p, size_t n) {

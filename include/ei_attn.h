@@ -98,7 +98,8 @@ int ei_attn_decode(ei_stream_t stream, const float* q, float* out, const float* 
 
 /* Ragged multi-sequence decode: sequence s reads its q at q + s*q_stride ([n_head][128]),
  * attends to cache rows kv_offset[s] .. kv_offset[s]+kv_len[s]-1 (kv_offset and kv_len
- * are device arrays; 1 <= kv_len[s] <= max_kv) and writes out + s*n_head*128.
+ * are device arrays; 0 <= kv_len[s] <= max_kv, a sequence with kv_len 0 gets zeros) and writes
+ * out + s*n_head*128.
  * No reference counterpart (the reference decodes one sequence); per sequence the
  * result is that of ei_attn_decode. */
 int ei_attn_decode_batched(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc,

@@ -156,12 +156,16 @@ def test_decode_long_context_split_combine(orc, gpu):
     assert ok16, msg16
 
 
-def test_decode_batched_ragged(orc, gpu):
-    import torch
-    H, HKV, nseq = 16, 8, 12
-    rng = np.random.default_rng(5)
+@pytest.mark.parametrize("nseq,empty", [(12, ()), (12, (3, 7)), (40, (0, 39))])
+def test_decode_batched_ragged(orc, gpu, nseq, empty):
+    """Ragged offsets and lengths; nseq 12 plans a key split per sequence, nseq 40 (320 (seq, KV
+    head) units) one workgroup each.  Sequences of length 0 (`empty`) must come out as zeros."""
+    H, HKV = 16, 8
+    rng = np.random.default_rng(5 + nseq)
     lens = rng.integers(1, 3000, nseq).astype(np.int32)
-    lens[0], lens[1] = 1, 64
+    lens[1], lens[2] = 1, 64
+    for i in empty:
+        lens[i] = 0
     gaps = rng.integers(0, 50, nseq)
     offs = np.zeros(nseq, np.int64)
     for i in range(1, nseq):
@@ -172,8 +176,11 @@ def test_decode_batched_ragged(orc, gpu):
     shape = gpu.AttnShape(H, HKV)
     ws = gpu.DecodeWorkspace(nseq, H, HKV, max_kv=int(lens.max()))
     out = _host(gpu.attn_decode_batched(_dev(q), _dev(k), _dev(v), _dev(offs), _dev(lens), shape, ws))
-    ref = orc.attn_decode_batched(q, k, v, offs, lens, H, HKV, D)
-    assert rel_err(out, ref) <= ATTN_RTOL
+    live = np.array([i for i in range(nseq) if i not in empty])
+    ref = orc.attn_decode_batched(q[live], k, v, offs[live], lens[live], H, HKV, D)
+    assert rel_err(out[live], ref) <= ATTN_RTOL
+    for i in empty:
+        assert not np.any(out[i]), f"sequence {i} of length 0 is not zeros"
 
 
 @pytest.mark.parametrize("H,HKV,T", [(32, 8, 1), (32, 8, 4096), (16, 8, 777), (4, 2, 55), (8, 1, 300)])
