@@ -201,7 +201,14 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         // group's last tile passes the other (stale) K buffer as Kn and discards sn: a straight-line
         // body keeps O in 64 VGPRs (a branch around either product makes the compiler
         // split O across register files and spill at two waves per SIMD).
-        auto step = [&](floatx16& s, floatx16& sn, int kt, const float* Kn, const float* Vt) {
+        // In-loop DMA for the next tiles: issued one or two instructions per MFMA sub-step, so
+        // their issue time hides under the matrix pipe instead of idling it.  kin / vin: a K
+        // (V) tile lies wholly below T and is fetched from scalar bases sbk / sbv into LDS at
+        // lbk / lbv (tiles reaching past T are fetched up front through the clamped path).
+        constexpr int NKI = 2 * DMA_PER_WAVE, NVI = DMA_PER_WAVE, NDI = NKI + NVI;
+        const int r0k = hw * 2 * DMA_PER_WAVE, i0v = hw * DMA_PER_WAVE;
+        auto step = [&](floatx16& s, floatx16& sn, int kt, const float* Kn, const float* Vt, bool kin, uint64_t sbk,
+                        uint32_t lbk, bool vin, uint64_t sbv, uint32_t lbv) {
             if (kt >= nfull) {  // tile crosses the diagonal (wave-uniform)
                 const int k0 = kt * kKT + 4 * hh;
 #pragma unroll
@@ -244,6 +251,15 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
             for (int r = 0; r < 16; ++r) {
                 const float4 kn = *reinterpret_cast<const float4*>(kp + 8 * ((r + 1) & 15));
                 const float4 vn = vrow((r + 1) & 15);
+#pragma unroll
+                for (int x = r * NDI / 16; x < (r + 1) * NDI / 16; ++x) {
+                    if (x < NKI) {
+                        if (kin && hh == 0)  // one padded K row per instruction (lanes 0..31)
+                            dma16_s(sbk + (uint64_t)x * row_bytes, voff_k, lbk + (r0k + x) * (kKS_F * 4));
+                    } else if (vin) {  // two V rows per instruction
+                        dma16_s(sbv + (uint64_t)(2 * (x - NKI)) * row_bytes, voff_v, lbv + (i0v + x - NKI) * 1024);
+                    }
+                }
                 __builtin_amdgcn_sched_barrier(0);  // step r+1's operands are read before step r's MFMAs
                 sn = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * r + 0], sn, 0, 0, 0);
                 o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, s[r], o[0], 0, 0, 0);
@@ -277,10 +293,18 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         floatx16 sa, sb;
         if (n_mine > 0) qk(gsm, sa);
         auto iter = [&](int i, floatx16& s, floatx16& sn) {
-            if (i + 2 < n_mine) dma_k(i + 2, i & 1);
-            if (i + 1 < n_mine) dma_v(i + 1, (i + 1) & 1);
+            const int tk = (kt_lo + kKS * (i + 2) + grp) * kKT, tv = (kt_lo + kKS * (i + 1) + grp) * kKT;
+            const bool kdo = i + 2 < n_mine, vdo = i + 1 < n_mine;
+            const bool kin = kdo && tk + kKT <= T, vin = vdo && tv + kKT <= T;
+            if (kdo && !kin) dma_k(i + 2, i & 1);
+            if (vdo && !vin) dma_v(i + 1, (i + 1) & 1);
+            const uint64_t sbk = kb_bytes + (uint64_t)(uint32_t)(tk + r0k) * row_bytes;
+            const uint64_t sbv = vb_bytes + (uint64_t)(uint32_t)(tv + 2 * i0v) * row_bytes;
+            const uint32_t lbk = __builtin_amdgcn_readfirstlane(lds_addr(gsm + (i & 1) * kKTileF));
+            const uint32_t lbv = __builtin_amdgcn_readfirstlane(lds_addr(gsv + ((i + 1) & 1) * kVTileF));
             if (i < n_mine)
-                step(s, sn, kt_lo + kKS * i + grp, gsm + ((i + 1) & 1) * kKTileF, gsv + (i & 1) * kVTileF);
+                step(s, sn, kt_lo + kKS * i + grp, gsm + ((i + 1) & 1) * kKTileF, gsv + (i & 1) * kVTileF, kin, sbk,
+                     lbk, vin, sbv, lbv);
             wait_vmcnt<0>();
             __syncthreads();
         };
