@@ -85,3 +85,33 @@ def test_e2e_logprob_hip_vs_reference(orc, gpu, n_head, n_head_kv):
     d = float(np.max(np.abs(hip - ref)))
     print(f"e2e H={n_head} HKV={n_head_kv}: max |d logprob| = {d:.3e} over {len(ref)} positions", flush=True)
     assert d <= LOGPROB_TOL, f"max |delta logprob| {d:.2e} > {LOGPROB_TOL}"
+
+
+@pytest.mark.gpu
+def test_serve_prefix_reuse_equals_generate(orc, gpu):
+    """The reference's serve invariant (tests/serve_test.py): a persistent server reusing the
+    KV rows of a cached common prefix produces the same greedy tokens as a fresh generate, on
+    this build's HIP attention; the generated tokens' logprobs agree within the e2e gate."""
+    import torch
+    from tests.tiny_qwen3 import PrefixServer, greedy_generate
+
+    model = TinyQwen3(seed=21, n_head=8, n_head_kv=2)
+    rng = np.random.default_rng(22)
+    n, chunk, n_ctx = 12, 32, 160
+    p1 = rng.integers(0, model.V, size=40)
+    factory = _hip_attention(model, gpu, torch)
+    srv = PrefixServer(model, factory, n_ctx, chunk)
+    t1, _, s1 = srv.request(p1, n)
+    p2 = np.concatenate([p1, np.array(t1[:5]), rng.integers(0, model.V, size=9)])  # continuation turn
+    p3 = p1.copy()                                                                 # same prompt again
+    p4 = rng.integers(0, model.V, size=23)                                         # unrelated prompt
+    cases = [("first", p1, t1, s1)]
+    for name, p in (("continuation", p2), ("same prompt", p3), ("unrelated", p4)):
+        t, lp, s = srv.request(p, n)
+        cases.append((name, p, t, s))
+        tf, lpf = greedy_generate(model, factory(n_ctx), p, n, chunk)
+        assert t == tf, f"{name}: serve {t} != generate {tf}"
+        d = float(np.max(np.abs(lp - lpf)))
+        assert d <= LOGPROB_TOL, f"{name}: |d logprob| {d:.2e}"
+    starts = {name: s for name, _, _, s in cases}
+    assert starts["continuation"] == len(p1) + 5 and starts["same prompt"] == len(p1) - 1 and starts["unrelated"] == 0

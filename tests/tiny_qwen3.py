@@ -132,3 +132,45 @@ def oracle_attention(model: TinyQwen3, O, scale: float | None = None, f64: bool 
         return attn
 
     return factory
+
+
+def greedy_generate(model: TinyQwen3, attn, prompt: np.ndarray, n: int, chunk: int, start: int = 0):
+    """The reference's generate/serve loop (src/main.cpp:497-531) on one attention instance:
+    evaluate prompt[start:] in chunks of `chunk` at positions start.. (rows [0, start) of the
+    caches are reused as they are), then n greedy steps.  Returns (tokens, logprobs of them)."""
+    pos = start
+    logits = None
+    while pos < len(prompt):
+        b = min(chunk, len(prompt) - pos)
+        logits = model.forward(prompt[pos:pos + b], pos, attn)
+        pos += b
+    toks, lps = [], []
+    last = logits[-1]
+    for _ in range(n):
+        z = last.astype(np.float64)
+        nxt = int(np.argmax(z))
+        zz = z - z.max()
+        lps.append(float(zz[nxt] - np.log(np.exp(zz).sum())))
+        toks.append(nxt)
+        last = model.forward(np.array([nxt]), pos, attn)[-1]
+        pos += 1
+    return toks, np.array(lps)
+
+
+class PrefixServer:
+    """Serve mode (src/main.cpp:497-531): one persistent attention instance; a request reuses
+    the cache rows of its longest common prefix with the cached tokens and re-evaluates at
+    least its last prompt token."""
+
+    def __init__(self, model: TinyQwen3, attn_factory, n_ctx: int, chunk: int):
+        self.model, self.attn, self.chunk = model, attn_factory(n_ctx), chunk
+        self.cached: list[int] = []
+
+    def request(self, prompt: np.ndarray, n: int):
+        common = 0
+        while common < min(len(self.cached), len(prompt)) and self.cached[common] == int(prompt[common]):
+            common += 1
+        start = min(common, len(prompt) - 1)
+        toks, lps = greedy_generate(self.model, self.attn, prompt, n, self.chunk, start)
+        self.cached = [int(t) for t in prompt] + toks[:-1]  # the last generated token is not evaluated
+        return toks, lps, start
