@@ -161,6 +161,38 @@ def decode_step(qkv: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, shape: At
     return out
 
 
+def attn_decode_paged(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, block_table: torch.Tensor,
+                      block_size: int, kv_len: torch.Tensor, shape: AttnShape, ws: DecodeWorkspace,
+                      scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Paged multi-sequence decode: block_table int32 [n_seq, max_blocks] of physical blocks of
+    `block_size` rows in the pool kc/vc; q [n_seq, >= H*128]; returns [n_seq, H, 128]."""
+    _need_gpu_f32("q", q)
+    n_seq, max_blocks = block_table.shape
+    out = torch.empty((n_seq, shape.n_head, HEAD_DIM), dtype=torch.float32, device=q.device) if out is None else out
+    scale = default_scale() if scale is None else scale
+    _capi.call("ei_attn_decode_paged", _stream(), q.data_ptr(), q.stride(0), out.data_ptr(), kc.data_ptr(),
+               vc.data_ptr(), block_table.data_ptr(), max_blocks, block_size, kv_len.data_ptr(), n_seq, shape.n_head,
+               shape.n_head_kv, shape.head_dim, float(scale), ws.max_kv, ws.buf.data_ptr(), ws.nbytes)
+    return out
+
+
+def decode_step_paged(qkv: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, block_table: torch.Tensor,
+                      block_size: int, kv_len: torch.Tensor, shape: AttnShape, q_gamma: torch.Tensor,
+                      k_gamma: torch.Tensor, cs: torch.Tensor, ws: DecodeWorkspace, scale: float | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused paged step: per sequence s, norm+RoPE at position kv_len[s]-1, append to its
+    physical row, attention over its kv_len[s] keys.  qkv [n_seq, (H+2HKV)*128]."""
+    _need_gpu_f32("qkv", qkv)
+    n_seq, max_blocks = block_table.shape
+    out = torch.empty((n_seq, shape.n_head, HEAD_DIM), dtype=torch.float32, device=qkv.device) if out is None else out
+    scale = default_scale() if scale is None else scale
+    _capi.call("ei_decode_step_paged", _stream(), qkv.data_ptr(), qkv.stride(0), out.data_ptr(), kc.data_ptr(),
+               vc.data_ptr(), block_table.data_ptr(), max_blocks, block_size, kv_len.data_ptr(), n_seq, shape.n_head,
+               shape.n_head_kv, shape.head_dim, q_gamma.data_ptr(), k_gamma.data_ptr(), cs.data_ptr(),
+               shape.rope_dim, float(shape.eps), float(scale), ws.max_kv, ws.buf.data_ptr(), ws.nbytes)
+    return out
+
+
 # ---------------------------------------------------------------- prefill
 class PrefillWorkspace:
     """Key-split shares for ei_attn_prefill_split: serves chunks of up to max_B rows with

@@ -236,6 +236,85 @@ EI_API int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride,
     return decode_common(static_cast<hipStream_t>(stream), a, n_seq, max_kv, ws, ws_bytes, true);
 }
 
+namespace {
+
+int check_paged(const int* block_table, int max_blocks, int block_size, const int* kv_len, int max_kv, int* shift) {
+    REQUIRE(block_table && kv_len, "block_table and kv_len are required");
+    REQUIRE(block_size >= 16 && (block_size & (block_size - 1)) == 0,
+            "block_size %d must be a power of two >= 16 (whole 16-key tiles per block)", block_size);
+    REQUIRE(max_blocks > 0 && (long)max_blocks * block_size >= max_kv,
+            "max_blocks %d x block_size %d does not cover max_kv %d", max_blocks, block_size, max_kv);
+    int sh = 0;
+    while ((1 << sh) < block_size) ++sh;
+    *shift = sh;
+    return EI_OK;
+}
+
+}  // namespace
+
+EI_API int ei_attn_decode_paged(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc,
+                                const float* vc, const int* block_table, int max_blocks, int block_size,
+                                const int* kv_len, int n_seq, int n_head, int n_head_kv, int head_dim, float scale,
+                                int max_kv, void* ws, size_t ws_bytes) {
+    if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
+    REQUIRE(q && out && kc && vc, "null pointer argument");
+    REQUIRE(n_seq > 0 && n_seq <= 65535, "n_seq %d out of range [1, 65535]", n_seq);
+    REQUIRE(q_stride >= (long)n_head * head_dim && q_stride % 4 == 0, "q_stride %ld", q_stride);
+    REQUIRE(aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc), "pointers must be 16-byte aligned");
+    int shift = 0;
+    if (int e = check_paged(block_table, max_blocks, block_size, kv_len, max_kv, &shift)) return e;
+    ei::DecodeArgs a{};
+    a.q = q;
+    a.q_stride = q_stride;
+    a.kc = const_cast<float*>(kc);
+    a.vc = const_cast<float*>(vc);
+    a.block_table = block_table;
+    a.max_blocks = max_blocks;
+    a.block_shift = shift;
+    a.kv_len = kv_len;
+    a.out = out;
+    a.H = n_head;
+    a.HKV = n_head_kv;
+    a.scale = scale;
+    return decode_common(static_cast<hipStream_t>(stream), a, n_seq, max_kv, ws, ws_bytes, false);
+}
+
+EI_API int ei_decode_step_paged(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc, float* vc,
+                                const int* block_table, int max_blocks, int block_size, const int* kv_len, int n_seq,
+                                int n_head, int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma,
+                                const float* cs, int rope_dim, float eps, float scale, int max_kv, void* ws,
+                                size_t ws_bytes) {
+    if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
+    if (int e = check_rope(rope_dim, head_dim)) return e;
+    REQUIRE(qkv && out && kc && vc && q_gamma && k_gamma && cs, "null pointer argument");
+    REQUIRE(n_seq > 0 && n_seq <= 65535, "n_seq %d out of range [1, 65535]", n_seq);
+    REQUIRE(row_stride >= (long)(n_head + 2 * n_head_kv) * head_dim, "row_stride %ld < (H+2*HKV)*head_dim",
+            row_stride);
+    REQUIRE(aligned16(qkv) && aligned16(out) && aligned16(kc) && aligned16(vc) && row_stride % 4 == 0,
+            "pointers and row_stride must be 16-byte aligned");
+    int shift = 0;
+    if (int e = check_paged(block_table, max_blocks, block_size, kv_len, max_kv, &shift)) return e;
+    ei::DecodeArgs a{};
+    a.q = qkv;
+    a.q_stride = row_stride;
+    a.kc = kc;
+    a.vc = vc;
+    a.block_table = block_table;
+    a.max_blocks = max_blocks;
+    a.block_shift = shift;
+    a.kv_len = kv_len;
+    a.out = out;
+    a.H = n_head;
+    a.HKV = n_head_kv;
+    a.scale = scale;
+    a.q_gamma = q_gamma;
+    a.k_gamma = k_gamma;
+    a.cs = reinterpret_cast<const float2*>(cs);
+    a.rope_dim = rope_dim;
+    a.eps = eps;
+    return decode_common(static_cast<hipStream_t>(stream), a, n_seq, max_kv, ws, ws_bytes, true);
+}
+
 EI_API int ei_attn_prefill(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc,
                            const float* vc, const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim,
                            float scale) {

@@ -113,10 +113,12 @@ __device__ __forceinline__ int tile_off(int row, int chunk) {
 }
 
 // Issue the 16 DMA instructions of one tile: K rows t0..t0+15 then V rows (two rows per
-// instruction), non-temporal: each byte of the cache is read once per step.  Rows past t_end are clamped to the last visible row (valid memory; their
+// instruction), non-temporal: each byte of the cache is read once per step.  p0 is the cache
+// row holding key t0; the tile's keys are consecutive rows from there (a paged block holds
+// whole 16-key tiles).  Rows past t_end are clamped to the last visible row (valid memory; their
 // scores are masked out).
 __device__ __forceinline__ void issue_tile(const float* slot, const float* kbase, const float* vbase, size_t KD,
-                                           int t0, int t_end, int lane) {
+                                           int t0, int t_end, int lane, size_t p0) {
     const int half = lane >> 5, s = lane & 31;
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(slot));
 #pragma unroll
@@ -124,14 +126,14 @@ __device__ __forceinline__ void issue_tile(const float* slot, const float* kbase
         const int row = 2 * t + half;
         const int key = min(t0 + row, t_end - 1);
         const int chunk = s ^ ((row & 1) << 3);
-        dma16_nt(kbase + (size_t)key * KD + 4 * chunk, base + t * 1024);
+        dma16_nt(kbase + (p0 + (size_t)(key - t0)) * KD + 4 * chunk, base + t * 1024);
     }
 #pragma unroll
     for (int t = 0; t < kTile / 2; ++t) {
         const int row = 2 * t + half;
         const int key = min(t0 + row, t_end - 1);
         const int chunk = s ^ ((row & 1) << 3);
-        dma16_nt(vbase + (size_t)key * KD + 4 * chunk, base + kTile * kHeadDim * 4 + t * 1024);
+        dma16_nt(vbase + (p0 + (size_t)(key - t0)) * KD + 4 * chunk, base + kTile * kHeadDim * 4 + t * 1024);
     }
 }
 
@@ -161,6 +163,12 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     const int len = a.kv_len ? a.kv_len[seq] : (*a.pos_dev + 1);
     const size_t KD = (size_t)a.HKV * D;
     const size_t row0 = a.kv_offset ? (size_t)a.kv_offset[seq] : 0;
+    // cache row of this sequence's key t: contiguous from row0, or through the block table
+    const int* btab = a.block_table ? a.block_table + (size_t)seq * a.max_blocks : nullptr;
+    const int bshift = a.block_shift, bmask = (1 << bshift) - 1;
+    auto phys = [&](int t) -> size_t {
+        return btab ? ((size_t)btab[t >> bshift] << bshift) | (size_t)(t & bmask) : (size_t)t;
+    };
     float* kbase = a.kc + row0 * KD + (size_t)kvh * D;
     float* vbase = a.vc + row0 * KD + (size_t)kvh * D;
     const int t_begin = split * a.chunk;
@@ -198,7 +206,8 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < kRing; ++i)
         if (tw0 + i * kStride < t_end) {
-            issue_tile(wring + i * kTileFloats, kbase, vbase, KD, tw0 + i * kStride, t_end, lane);
+            issue_tile(wring + i * kTileFloats, kbase, vbase, KD, tw0 + i * kStride, t_end, lane,
+                       phys(tw0 + i * kStride));
             ++ntiles0;
         }
     if (w <= 1) {  // this wave's prologue DMA (older than its tiles) has landed
@@ -224,7 +233,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
         }
         __syncthreads();
         if (owner && tid < 2 * D) {
-            float* dst = (tid < D ? kbase : vbase) + (size_t)pos * KD + (tid & (D - 1));
+            float* dst = (tid < D ? kbase : vbase) + phys(pos) * KD + (tid & (D - 1));
             *dst = knew[tid >> 7][tid & (D - 1)];
         }
     }
@@ -329,7 +338,8 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
         // refill is issued into it
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_wave_barrier();
-        if (t0 + kRing * kStride < t_end) issue_tile(tk, kbase, vbase, KD, t0 + kRing * kStride, t_end, lane);
+        if (t0 + kRing * kStride < t_end)
+            issue_tile(tk, kbase, vbase, KD, t0 + kRing * kStride, t_end, lane, phys(t0 + kRing * kStride));
     }
 
     // ---- wave partial: l summed over the lanes holding each head; merge the waves in LDS

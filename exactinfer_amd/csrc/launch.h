@@ -36,6 +36,9 @@ struct DecodeArgs {
     float* kc;              // cache base (rows of HKV*128 floats)
     float* vc;
     const int64_t* kv_offset;  // per-sequence first cache row, or null (0)
+    const int* block_table;    // paged: [n_seq][max_blocks] physical block of each logical block, or null
+    int max_blocks;
+    int block_shift;           // paged: log2(block size), block size a power of two >= 16
     const int* kv_len;         // per-sequence visible keys, or null (then *pos_dev + 1)
     const int* pos_dev;
     float* out;             // [n_seq][H][128]

@@ -118,6 +118,25 @@ int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride, float*
                    int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma, const float* cs,
                    int rope_dim, float eps, float scale, int max_kv, void* ws, size_t ws_bytes);
 
+/* ------------------------------------------------------------------ paged KV (multi-sequence serving)
+ * Sequence s's key t lives in cache row block_table[s*max_blocks + t/block_size]*block_size
+ * + t%block_size of the shared pool kc/vc (rows of n_head_kv*128 floats); block_size is a
+ * power of two >= 16, max_blocks*block_size >= max_kv, 0 <= kv_len[s] <= max_kv (kv_len
+ * 0 gives zeros).  Sequences may share physical blocks (a common prefix cached once).  The
+ * reference decodes one contiguous sequence (src/cuda/model_cuda.cu:1043-1111); these are
+ * the serve-side extension of ei_attn_decode_batched and ei_decode_step: per sequence the
+ * result is that of ei_attn_decode on the gathered rows.  ei_decode_step_paged writes the
+ * new K/V row of sequence s (logical position kv_len[s]-1) to its physical row, so that
+ * row's block must be private to the sequence. */
+int ei_attn_decode_paged(ei_stream_t stream, const float* q, long q_stride, float* out, const float* kc,
+                         const float* vc, const int* block_table, int max_blocks, int block_size, const int* kv_len,
+                         int n_seq, int n_head, int n_head_kv, int head_dim, float scale, int max_kv, void* ws,
+                         size_t ws_bytes);
+int ei_decode_step_paged(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc, float* vc,
+                         const int* block_table, int max_blocks, int block_size, const int* kv_len, int n_seq,
+                         int n_head, int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma,
+                         const float* cs, int rope_dim, float eps, float scale, int max_kv, void* ws, size_t ws_bytes);
+
 /* ------------------------------------------------------------------ causal prefill
  * B query rows (row b at q + b*q_stride, heads [n_head][128], already normed + roped) at
  * positions *pos_dev + b; query b attends to cache rows 0 .. *pos_dev + b (the whole

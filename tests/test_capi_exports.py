@@ -85,3 +85,14 @@ def test_prefill_split_workspace_contract():
         _capi.call("ei_attn_prefill_split", None, p, 4096, p, p, p, p, 512, 32, 8, 128, 0.1, 2048, p, 16)
     with pytest.raises(_capi.EiError, match="max_kv"):
         _capi.call("ei_attn_prefill_split", None, p, 4096, p, p, p, p, 512, 32, 8, 128, 0.1, 100, p, 1 << 30)
+
+
+def test_paged_argument_errors():
+    from exactinfer_amd import _capi
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    with pytest.raises(_capi.EiError, match="block_size 24"):
+        _capi.call("ei_attn_decode_paged", None, p, 4096, p, p, p, p, 8, 24, p, 2, 32, 8, 128, 0.1, 128, p, 1 << 20)
+    with pytest.raises(_capi.EiError, match="does not cover max_kv"):
+        _capi.call("ei_attn_decode_paged", None, p, 4096, p, p, p, p, 4, 16, p, 2, 32, 8, 128, 0.1, 128, p, 1 << 20)
+    with pytest.raises(_capi.EiError, match="block_table and kv_len"):
+        _capi.call("ei_attn_decode_paged", None, p, 4096, p, p, p, None, 8, 16, p, 2, 32, 8, 128, 0.1, 128, p, 1 << 20)

@@ -356,3 +356,86 @@ def test_prefill_split_graph_replays_track_position(orc, gpu):
         torch.cuda.synchronize()
         ref = orc.attn_prefill(qh, k, v, B, p0, H, HKV, D)
         assert rel_err(_host(out), ref) <= ATTN_RTOL, f"pos0 {p0}"
+
+
+# ---------------------------------------------------------------- paged KV (multi-sequence serving)
+def _paged_layout(rng, lens, bs, shared_prefix_blocks, spare=3):
+    """Block tables over a shuffled pool: sequences 0 and 1 share their first blocks."""
+    nseq = len(lens)
+    nblk = [max(1, -(-int(n) // bs)) for n in lens]
+    max_blocks = max(nblk)
+    total = sum(nblk) + spare
+    perm = rng.permutation(total)
+    table = np.zeros((nseq, max_blocks), np.int32)
+    k = 0
+    for s in range(nseq):
+        for j in range(nblk[s]):
+            if s == 1 and j < shared_prefix_blocks:
+                table[s, j] = table[0, j]
+            else:
+                table[s, j] = perm[k]
+                k += 1
+    return table, total
+
+
+def _gather(pool, table, s, n, bs):
+    rows = [table[s, t // bs] * bs + t % bs for t in range(n)]
+    return pool[rows]
+
+
+@pytest.mark.parametrize("bs", [16, 64])
+def test_decode_paged_matches_reference(orc, gpu, bs):
+    H, HKV = 16, 8
+    rng = np.random.default_rng(40 + bs)
+    lens = np.array([700, 300, 1, 0, 129, 2048, 64], np.int32)
+    shared = 3  # sequences 0 and 1 share their first 3 blocks (a cached common prefix)
+    lens[1] = max(lens[1], shared * bs + 5)
+    table, nblocks = _paged_layout(rng, lens, bs, shared)
+    pool_k, pool_v = _cache(orc, nblocks * bs, HKV, 4000 + bs)
+    q = orc.normal((len(lens), H * D), 4001)
+    shape = gpu.AttnShape(H, HKV)
+    ws = gpu.DecodeWorkspace(len(lens), H, HKV, max_kv=int(lens.max()))
+    out = _host(gpu.attn_decode_paged(_dev(q), _dev(pool_k), _dev(pool_v), _dev(table), bs, _dev(lens), shape, ws))
+    for s, n in enumerate(lens):
+        if n == 0:
+            assert not np.any(out[s])
+            continue
+        kk, vv = _gather(pool_k, table, s, n, bs), _gather(pool_v, table, s, n, bs)
+        ref = orc.attn_decode(q[s].reshape(H, D), kk, vv, int(n), H, HKV, D)
+        assert rel_err(out[s], ref) <= ATTN_RTOL, f"sequence {s} (len {n})"
+
+
+def test_decode_step_paged_appends_to_physical_rows(orc, gpu):
+    """Fused paged step: each sequence's new K/V row lands in its physical row (bit-exact),
+    the shared prefix blocks and every other row stay untouched, attention sees the append."""
+    H, HKV, bs = 32, 8, 32
+    rng = np.random.default_rng(41)
+    lens = np.array([400, 150, 33, 1], np.int32)  # after the append (the new token included)
+    shared = 2
+    table, nblocks = _paged_layout(rng, lens, bs, shared)
+    n_rows = nblocks * bs
+    pool_k, pool_v = _cache(orc, n_rows, HKV, 4100)
+    qkv = orc.normal((len(lens), (H + 2 * HKV) * D), 4101)
+    qg, kg = orc.gamma(D, 5), orc.gamma(D, 6)
+    cs = gpu.rope_table(int(lens.max()))
+    shape = gpu.AttnShape(H, HKV)
+    ws = gpu.DecodeWorkspace(len(lens), H, HKV, max_kv=int(lens.max()))
+    kd, vd = _dev(pool_k), _dev(pool_v)
+    out = _host(gpu.decode_step_paged(_dev(qkv), kd, vd, _dev(table), bs, _dev(lens), shape, _dev(qg), _dev(kg), cs,
+                                      ws))
+    rk, rv = pool_k.reshape(n_rows, -1).copy(), pool_v.reshape(n_rows, -1).copy()
+    normed = []
+    for s, n in enumerate(lens):
+        pos = int(n) - 1
+        row = orc.headnorm_rope(qkv[s:s + 1], H, D, qg, pos, 128, 1e6, 1e-6)
+        row = orc.headnorm_rope(row, HKV, D, kg, pos, 128, 1e6, 1e-6, col0=H * D)
+        phys = table[s, pos // bs] * bs + pos % bs
+        rk[phys] = row[0, H * D:(H + HKV) * D]
+        rv[phys] = row[0, (H + HKV) * D:]
+        normed.append(row)
+    assert bits_equal(_host(kd).reshape(n_rows, -1), rk) and bits_equal(_host(vd).reshape(n_rows, -1), rv)
+    for s, n in enumerate(lens):
+        kk = _gather(rk.reshape(n_rows, HKV, D), table, s, n, bs)
+        vv = _gather(rv.reshape(n_rows, HKV, D), table, s, n, bs)
+        ref = orc.attn_decode(normed[s][0, :H * D].reshape(H, D), kk, vv, int(n), H, HKV, D)
+        assert rel_err(out[s], ref) <= ATTN_RTOL, f"sequence {s}"
