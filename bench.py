@@ -47,7 +47,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch the per-layer kernels eagerly")
     ap.add_argument("--extra", action="store_true", help="also measure configs[3] and configs[4]")
-    ap.add_argument("--only", choices=["decode", "prefill", "prefill-chunked", "longctx", "batched"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill-chunked", "longctx", "batched", "batched-paged"],
+                    default=None)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
     return ap.parse_args()
@@ -155,8 +156,9 @@ def bench_decode(torch, A, H, HKV, n_layer, ctx, steps, warmup, use_graph, spike
     }
 
 
-def bench_batched(torch, A, steps, warmup, use_graph, seed=3000):
-    """1.7B shape, 64 sequences with kv_len ~ U[256, 8192], 28 layers."""
+def bench_batched(torch, A, steps, warmup, use_graph, seed=3000, block_size=0):
+    """1.7B shape, 64 sequences with kv_len ~ U[256, 8192], 28 layers.  block_size > 0: the same
+    sequences in a paged pool (shuffled blocks of block_size rows, fused paged step)."""
     import numpy as np
     H, HKV, n_layer, nseq = 16, 8, 28, 64
     shape = A.AttnShape(H, HKV)
@@ -166,6 +168,8 @@ def bench_batched(torch, A, steps, warmup, use_graph, seed=3000):
     rows = int(lens.sum())
     kd = HKV * D
     dev = "cuda"
+    if block_size:
+        rows = sum(-(-int(n) // block_size) for n in lens) * block_size
     kc = torch.empty((n_layer, rows, kd), dtype=torch.float32, device=dev)
     vc = torch.empty_like(kc)
     for l in range(n_layer):
@@ -176,12 +180,27 @@ def bench_batched(torch, A, steps, warmup, use_graph, seed=3000):
     cs = A.rope_table(int(lens.max()), device=dev)
     off_d = torch.from_numpy(offs).to(dev)
     len_d = torch.from_numpy(lens).to(dev)
+    table_d = None
+    if block_size:
+        # each sequence's rows in whole blocks; the blocks of all sequences shuffled over the pool
+        nblk = [-(-int(n) // block_size) for n in lens]
+        perm = rng.permutation(sum(nblk)).astype(np.int32)
+        table = np.zeros((nseq, max(nblk)), np.int32)
+        k = 0
+        for si in range(nseq):
+            table[si, :nblk[si]] = perm[k:k + nblk[si]]
+            k += nblk[si]
+        table_d = torch.from_numpy(table).to(dev)
     out = torch.empty((n_layer, nseq, H, D), dtype=torch.float32, device=dev)
     ws = [A.DecodeWorkspace(nseq, H, HKV, int(lens.max()), device=dev) for _ in range(n_layer)]
 
     def layer(l):
-        A.decode_step(qkv[l], kc[l], vc[l], shape, gam[0], gam[1], cs, ws[l], kv_offset=off_d, kv_len=len_d,
-                      out=out[l])
+        if table_d is not None:
+            A.decode_step_paged(qkv[l], kc[l], vc[l], table_d, block_size, len_d, shape, gam[0], gam[1], cs, ws[l],
+                                out=out[l])
+        else:
+            A.decode_step(qkv[l], kc[l], vc[l], shape, gam[0], gam[1], cs, ws[l], kv_offset=off_d, kv_len=len_d,
+                          out=out[l])
 
     def step():
         for l in range(n_layer):
@@ -207,7 +226,7 @@ def bench_batched(torch, A, steps, warmup, use_graph, seed=3000):
     kern_ms = ms / n_layer
     return {"ms_per_step": ms, "gbs": bytes_layer * n_layer / (ms * 1e-3) / 1e9, "kernel_ms": kern_ms,
             "kernel_gbs": bytes_layer / (kern_ms * 1e-3) / 1e9, "bytes_per_launch": bytes_layer,
-            "sum_kv_len": int(lens.sum())}
+            "sum_kv_len": int(lens.sum()), "block_size": block_size}
 
 
 # ---------------------------------------------------------------- prefill
@@ -346,6 +365,11 @@ def main():
         log("batched ragged decode configs[4] ...")
         res["batched"] = bench_batched(torch, A, 128 if args.steps >= 128 else args.steps, 3, use_graph)
         log(json.dumps(res["batched"]))
+    if args.extra or args.only == "batched-paged":
+        log("batched ragged decode configs[4], paged KV (64-row blocks, shuffled) ...")
+        res["batched_paged"] = bench_batched(torch, A, 128 if args.steps >= 128 else args.steps, 3, use_graph,
+                                             block_size=64)
+        log(json.dumps(res["batched_paged"]))
     if args.only not in (None, "decode"):
         print(json.dumps(res))
         return

@@ -145,7 +145,7 @@ int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void
     REQUIRE(ws != nullptr && aligned16(ws), "workspace missing or not 16-byte aligned");
     const size_t need = ei::decode_ws_bytes(n_seq, a.H, a.HKV, max_kv);
     REQUIRE(ws_bytes >= need, "workspace of %zu bytes < %zu needed (ei_attn_decode_ws_bytes)", ws_bytes, need);
-    const ei::DecodePlan p = ei::decode_plan(n_seq, a.HKV, max_kv);
+    const ei::DecodePlan p = ei::decode_plan(n_seq, a.HKV, max_kv, a.block_table != nullptr);
     const size_t slots = (size_t)n_seq * a.HKV * p.nsplit;
     const int G = a.H / a.HKV;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -244,6 +244,8 @@ int check_paged(const int* block_table, int max_blocks, int block_size, const in
             "block_size %d must be a power of two >= 16 (whole 16-key tiles per block)", block_size);
     REQUIRE(max_blocks > 0 && (long)max_blocks * block_size >= max_kv,
             "max_blocks %d x block_size %d does not cover max_kv %d", max_blocks, block_size, max_kv);
+    REQUIRE(max_kv > 0 && (long)max_kv <= (long)ei::kDecodeMaxSplits * ei::kDecodePagedMaxChunk,
+            "max_kv %d out of range for paged decode", max_kv);
     int sh = 0;
     while ((1 << sh) < block_size) ++sh;
     *shift = sh;

@@ -184,6 +184,16 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     // anything before the whole workgroup's 128 KB is in flight
     const int tw0 = t_begin + kTile * w;
     constexpr int kStride = kTile * kWaves;  // distance between a wave's consecutive tiles
+    // paged: lane i holds the cache row of this wave's tile i (the plan keeps <= 64 tiles per
+    // wave), read back with readlane: one table load per wave instead of one per tile
+    int lane_row = 0;
+    if (btab) {
+        const int t = min(tw0 + lane * kStride, max(t_end - 1, 0));
+        lane_row = (btab[t >> bshift] << bshift) | (t & bmask);
+    }
+    auto tile_row = [&](int t0) -> size_t {
+        return btab ? (size_t)(uint32_t)__builtin_amdgcn_readlane(lane_row, (t0 - tw0) / kStride) : (size_t)t0;
+    };
     const bool owner = FUSED && t_begin <= pos && pos < t_end;
     if (w == 0) {
         const uint32_t qa = __builtin_amdgcn_readfirstlane(lds_addr(qs));
@@ -207,7 +217,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     for (int i = 0; i < kRing; ++i)
         if (tw0 + i * kStride < t_end) {
             issue_tile(wring + i * kTileFloats, kbase, vbase, KD, tw0 + i * kStride, t_end, lane,
-                       phys(tw0 + i * kStride));
+                       tile_row(tw0 + i * kStride));
             ++ntiles0;
         }
     if (w <= 1) {  // this wave's prologue DMA (older than its tiles) has landed
@@ -339,7 +349,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_wave_barrier();
         if (t0 + kRing * kStride < t_end)
-            issue_tile(tk, kbase, vbase, KD, t0 + kRing * kStride, t_end, lane, phys(t0 + kRing * kStride));
+            issue_tile(tk, kbase, vbase, KD, t0 + kRing * kStride, t_end, lane, tile_row(t0 + kRing * kStride));
     }
 
     // ---- wave partial: l summed over the lanes holding each head; merge the waves in LDS
@@ -475,7 +485,7 @@ static int pow2_ceil(long x) {
     return p;
 }
 
-DecodePlan decode_plan(int n_seq, int HKV, int max_kv) {
+DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged) {
     // One workgroup per (sequence, KV head) streams the most bytes per launch and needs no
     // combine; keys are split only as far as it takes to reach about one workgroup per CU
     // (256): chunk = max_kv / ceil(256 / (n_seq * HKV)), rounded up to a power of two >= 128
@@ -489,6 +499,8 @@ DecodePlan decode_plan(int n_seq, int HKV, int max_kv) {
         const int v = std::atoi(env);
         if (v >= 64 && v % 64 == 0) chunk = v;
     }
+    // paged: a wave keeps the cache rows of its tiles in one register (<= 64 tiles, 4 waves)
+    if (paged && chunk > kDecodePagedMaxChunk) chunk = kDecodePagedMaxChunk;
     while (((long)max_kv + chunk - 1) / chunk > kDecodeMaxSplits) chunk *= 2;
     DecodePlan p;
     p.chunk = chunk;
@@ -500,7 +512,9 @@ DecodePlan decode_plan(int n_seq, int HKV, int max_kv) {
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv) {
-    const DecodePlan p = decode_plan(n_seq, HKV, max_kv);
+    // sized for the larger of the paged and contiguous plans, so one workspace serves both
+    const DecodePlan p0 = decode_plan(n_seq, HKV, max_kv, false), p1 = decode_plan(n_seq, HKV, max_kv, true);
+    const DecodePlan p = p0.nsplit >= p1.nsplit ? p0 : p1;
     const size_t slots = (size_t)n_seq * HKV * p.nsplit;
     const int G = H / HKV;
     return align256(slots * G * kHeadDim * 4) + align256(slots * G * 2 * 4);

@@ -27,7 +27,8 @@ struct DecodePlan {
     int nsplit;
 };
 constexpr int kDecodeMaxSplits = 256;
-DecodePlan decode_plan(int n_seq, int HKV, int max_kv);
+constexpr int kDecodePagedMaxChunk = 4096;  // 4 waves x 64 tiles of 16 keys
+DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged);
 size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv);
 
 struct DecodeArgs {
