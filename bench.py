@@ -29,7 +29,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 # the factor a plain 256 MiB copy needs (FETCH x2.000, WRITE x1.000); profiles/*_hbm_traffic.md
 # and profiles/prefill_configs2_kernel_trace.md hold the runs.
 TRAFFIC_DECODE_PER_LAYER = (16539 + 303.5) * 2.0 * 1024 + (528 + 16) * 1024  # k_decode + k_combine
-TRAFFIC_PREFILL = 24681 * 2.0 * 1024 + 32770 * 1024                          # k_prefill
+TRAFFIC_PREFILL = 24704 * 2.0 * 1024 + 32773 * 1024                          # k_prefill
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 D = 128
 
