@@ -326,7 +326,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the attention path has no multi-GPU leg in this build "
-              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+              "(one process per GPU would shard decode by KV head and prefill by head); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
     from exactinfer_amd import attention as A
