@@ -46,7 +46,9 @@ def parse():
     ap.add_argument("--prefill-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch the per-layer kernels eagerly")
-    ap.add_argument("--extra", action="store_true", help="also measure configs[3] and configs[4]")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the parity-case shapes reported beside the headline (configs[3], configs[4] contiguous "
+                         "and paged, configs[2] in 512-token chunks)")
     ap.add_argument("--only", choices=["decode", "prefill", "prefill-chunked", "longctx", "batched", "batched-paged"],
                     default=None)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
@@ -351,21 +353,22 @@ def main():
         log("prefill configs[2] ...")
         res["prefill"] = bench_prefill(torch, A, 32, 8, 36, 2048, args.prefill_steps, 1)
         log(json.dumps(res["prefill"]))
-    if args.extra or args.only == "prefill-chunked":
+    extra = args.only is None and not args.no_extra
+    if extra or args.only == "prefill-chunked":
         log("prefill configs[2] in 512-token chunks ...")
         res["prefill_chunked"] = bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512)
         log(json.dumps(res["prefill_chunked"]))
         log(json.dumps(bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512, split=False)))
-    if args.extra or args.only == "longctx":
+    if extra or args.only == "longctx":
         log("long-context decode configs[3] ...")
         res["longctx"] = bench_decode(torch, A, 16, 8, 28, 32768, max(8, args.steps // 8), 3, use_graph,
                                       spike_every=512, seed=4000)
         log(json.dumps(res["longctx"]))
-    if args.extra or args.only == "batched":
+    if extra or args.only == "batched":
         log("batched ragged decode configs[4] ...")
         res["batched"] = bench_batched(torch, A, 128 if args.steps >= 128 else args.steps, 3, use_graph)
         log(json.dumps(res["batched"]))
-    if args.extra or args.only == "batched-paged":
+    if extra or args.only == "batched-paged":
         log("batched ragged decode configs[4], paged KV (64-row blocks, shuffled) ...")
         res["batched_paged"] = bench_batched(torch, A, 128 if args.steps >= 128 else args.steps, 3, use_graph,
                                              block_size=64)
@@ -408,9 +411,15 @@ def main():
                                         "traffic": TRAFFIC_PREFILL, "kernel": "k_prefill<4>",
                                         "kernel_us": round(pre["kernel_ms"] * 1e3, 2),
                                         "flops_per_launch": pre["flops_per_launch"]}}
-    for k in ("longctx", "batched"):
+    # the other configs (parity-test shapes), measured beside the headline for context
+    ex = {}
+    for k in ("longctx", "batched", "batched_paged", "prefill_chunked"):
         if k in res:
-            line[k] = {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in res[k].items()}
+            ex[k] = {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in res[k].items()}
+            if "gbs" in res[k]:
+                ex[k]["pct_hbm_peak"] = round(100 * res[k]["gbs"] / HBM_PEAK_GBS, 2)
+    if ex:
+        line["extra"] = ex
     print(json.dumps(line), flush=True)
 
 
