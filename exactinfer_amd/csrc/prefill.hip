@@ -19,8 +19,13 @@
 // Workgroup = KS key groups x GW query heads (the GW heads of one KV head that share every
 // K/V tile).  Key group g takes the tiles kt = KS*i + g of the block's causal range and
 // keeps its own (m, l, O); the groups merge through LDS at the end of the block.  With
-// KS = 2 every SIMD runs two waves, so one wave's softmax VALU work and LDS waits overlap
-// the other's matrix instructions.
+// KS = 2 every SIMD runs two waves whose matrix streams interleave, each covering the
+// other's LDS waits and per-tile softmax preamble.  Inside a wave's stream the next score
+// chain alternates with this tile's P.V chains, and the next tiles' DMA instructions are
+// issued between them (on this part VALU or VMEM work outside the stream idles the pipe).
+// For short chunks at long positions (ei_attn_prefill_split) the key range of every block
+// is further split over ksplit workgroups whose unnormalised shares k_prefill_combine
+// merges.
 //
 // K/V tiles (32 keys) reach LDS by LDS DMA (global_load_lds_dwordx4) straight from the
 // cache, two tiles ahead for K and one for V, per key group:
