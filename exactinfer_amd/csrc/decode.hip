@@ -1,19 +1,23 @@
 // decode.hip — split-K decode attention for gfx950 (one query token per sequence).
 //
-// Work decomposition: grid (nsplit, HKV, n_seq), 256 threads (4 waves).  A workgroup owns
-// one KV head of one sequence and one chunk of keys, and serves all G = H/HKV query heads
-// of that GQA group from the same K/V bytes (the reference re-reads K/V once per query
-// head, src/cuda/model_cuda.cu:1051, :1066).  Inside the chunk, wave w owns the 16-key
-// tiles w, w+4, w+8, ... and runs its own online softmax over them; the four waves merge
-// once at the end.  There is no workgroup barrier in the key loop.
+// Work decomposition: grid (nsplit, HKV, n_seq); 4 waves (long chunks, each wave a two-tile
+// ring) or 8 waves (chunks of <= 128 keys, one tile per wave).  A workgroup owns one KV head
+// of one sequence and one chunk of keys, and serves all G = H/HKV query heads of that GQA
+// group from the same K/V bytes (the reference re-reads K/V once per query head,
+// src/cuda/model_cuda.cu:1051, :1066).  Inside the chunk, wave w owns the 16-key tiles
+// w, w+NW, w+2NW, ... and runs its own online softmax over them; the waves merge once at
+// the end.  There is no workgroup barrier in the key loop.  The split plan gives every
+// (sequence, KV head) its own workgroup first and cuts keys only as far as it takes to
+// reach about one workgroup per CU.
 //
 // Data movement: each wave streams its tiles HBM -> LDS with global_load_lds_dwordx4
 // (gfx950 LDS DMA: 64 lanes x 16 B = one 1 KB instruction, no VGPRs spent on landing
-// data), through a private two-slot ring (2 x 16 KB), so a workgroup keeps 128 KB of K/V
-// in flight.  A 16-key tile is 16 rows x 512 B of K and the same of V; every instruction
-// moves two whole rows (fully used 128-byte lines).  Within a row, 16-byte chunk q is
-// stored at slot q ^ 8*(row & 1), which keeps both read patterns below free of LDS bank
-// conflicts between neighbouring rows.
+// data, non-temporal: each byte is read once per step), through a private ring, so a
+// workgroup keeps 128 KB of K/V in flight.  A 16-key tile is 16 rows x 512 B of K and the
+// same of V; every instruction moves two whole rows (fully used 128-byte lines).  Within a
+// row, 16-byte chunk q is stored at slot q ^ 8*(row & 1), which keeps both read patterns
+// below free of LDS bank conflicts between neighbouring rows.  Cache rows come from a
+// per-sequence offset (contiguous ranges) or from a block table (paged pools).
 //
 //   scores    lane (r = l/8, c = l%8) reads rows r and r+8 at d = 4c + 32i (i < 4) and
 //             holds q for those d in registers; the 8 lanes of a row hold partial dots for
@@ -37,6 +41,7 @@
 // Fused variant: the workgroup also applies QK-norm + RoPE to its G query heads, and the
 // workgroup whose chunk holds the new position writes the normed K row and the V row to
 // the cache and patches them into its LDS tile (the DMA may have read the old bytes).
+// A sequence of length 0 (ragged or paged batches) produces zeros.
 #include "common.h"
 #include "launch.h"
 
