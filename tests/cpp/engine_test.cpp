@@ -5,7 +5,10 @@
 // layer running QK-norm + RoPE, KV append and attention (src/cuda/model_cuda.cu:1797-1822),
 // while the CPU reference processes the same tokens one at a time (src/model.cpp:138-140,
 // :176-214).  Checks: attention rows within 1e-5 (relative to max(|ref|, row rms)), KV caches
-// bit-exact, and the reference's error behaviour (out_of_range past n_ctx).
+// bit-exact, and the reference's error behaviour (out_of_range past n_ctx).  Where the
+// reference's own sequential fp32 sums drift past 1e-5 (long contexts), a row passes when
+// it is within 1e-5 of float64 attention and no farther from it than the reference is
+// (the rule of tests/parity.py).
 //
 // Usage: engine_test <n_layer> <n_head> <n_head_kv> <prompt> <max_batch> <decode_steps> <n_ctx>
 // Prints one JSON line; exit status 0 when every check passes.
@@ -69,6 +72,7 @@ int main(int argc, char** argv) {
     // ---- CPU reference, one token at a time
     std::vector<float> rk(size_t(L) * n_ctx * KD, 0.f), rv(size_t(L) * n_ctx * KD, 0.f);
     std::vector<float> ratt(size_t(L) * total * H * D);
+    std::vector<float> rq(size_t(L) * total * H * D);  // normed, roped q of every (layer, token)
     std::vector<float> row(QKV), sc(size_t(H) * n_ctx);
     for (int t = 0; t < total; ++t)
         for (int l = 0; l < L; ++l) {
@@ -81,12 +85,14 @@ int main(int argc, char** argv) {
             orc_kv_append(row.data() + size_t(H) * D, row.data() + size_t(H + HKV) * D, QKV, 1, kc, vc, KD, t);
             orc_attn_decode(row.data(), kc, vc, ratt.data() + (size_t(l) * total + t) * H * D, t + 1, H, HKV, D,
                             scale, sc.data());
+            std::copy(row.data(), row.data() + size_t(H) * D, rq.begin() + (size_t(l) * total + t) * H * D);
         }
 
     // ---- GPU engine: prompt in chunks, then decode steps
     hipStream_t st;
     hc(hipStreamCreate(&st));
     double worst = 0;
+    int fallback_rows = 0;
     bool caches_exact = true, threw_ok = false;
     {
         ei::HipAttention eng(cfg, n_ctx, max_batch, st);
@@ -107,11 +113,31 @@ int main(int argc, char** argv) {
                 eng.layer(l, d_qkv, QKV, d_qg + size_t(l) * D, d_kg + size_t(l) * D, d_att);
                 hc(hipMemcpyAsync(ha.data(), d_att, size_t(B) * H * D * 4, hipMemcpyDeviceToHost, st));
                 hc(hipStreamSynchronize(st));
-                for (int b = 0; b < B; ++b)
+                for (int b = 0; b < B; ++b) {
+                    const int t = pos0 + b;
+                    double row_worst = 0;
                     for (int h = 0; h < H; ++h) {
-                        const float* ref = ratt.data() + ((size_t(l) * total + pos0 + b) * H + h) * D;
-                        worst = std::max(worst, rel_err_row(ha.data() + (size_t(b) * H + h) * D, ref, D));
+                        const float* ref = ratt.data() + ((size_t(l) * total + t) * H + h) * D;
+                        row_worst = std::max(row_worst, rel_err_row(ha.data() + (size_t(b) * H + h) * D, ref, D));
                     }
+                    if (row_worst > 1e-5) {  // long-context fallback against float64
+                        std::vector<double> ex(size_t(H) * D);
+                        std::vector<float> exf(size_t(H) * D);
+                        orc_attn_f64(rq.data() + (size_t(l) * total + t) * H * D, rk.data() + size_t(l) * n_ctx * KD,
+                                     rv.data() + size_t(l) * n_ctx * KD, ex.data(), t + 1, H, HKV, D, scale);
+                        for (size_t i = 0; i < ex.size(); ++i) exf[i] = float(ex[i]);
+                        double got_x = 0, ref_x = 0;
+                        for (int h = 0; h < H; ++h) {
+                            const float* x = exf.data() + size_t(h) * D;
+                            got_x = std::max(got_x, rel_err_row(ha.data() + (size_t(b) * H + h) * D, x, D));
+                            ref_x = std::max(ref_x,
+                                             rel_err_row(ratt.data() + ((size_t(l) * total + t) * H + h) * D, x, D));
+                        }
+                        ++fallback_rows;
+                        if (got_x <= 1e-5 && got_x <= ref_x) row_worst = got_x;
+                    }
+                    worst = std::max(worst, row_worst);
+                }
             }
         };
         for (int p = 0; p < prompt; p += max_batch) run_chunk(p, std::min(max_batch, prompt - p));
@@ -142,9 +168,10 @@ int main(int argc, char** argv) {
     }
     hc(hipStreamDestroy(st));
     const bool ok = worst <= 1e-5 && caches_exact && threw_ok;
-    std::printf("{\"ok\": %s, \"max_rel_err\": %.3e, \"caches_bit_exact\": %s, \"out_of_range_thrown\": %s, "
-                "\"layers\": %d, \"prompt\": %d, \"max_batch\": %d, \"decode_steps\": %d}\n",
-                ok ? "true" : "false", worst, caches_exact ? "true" : "false", threw_ok ? "true" : "false", L, prompt,
-                max_batch, steps);
+    std::printf("{\"ok\": %s, \"max_rel_err\": %.3e, \"f64_fallback_rows\": %d, \"caches_bit_exact\": %s, "
+                "\"out_of_range_thrown\": %s, \"layers\": %d, \"prompt\": %d, \"max_batch\": %d, "
+                "\"decode_steps\": %d}\n",
+                ok ? "true" : "false", worst, fallback_rows, caches_exact ? "true" : "false",
+                threw_ok ? "true" : "false", L, prompt, max_batch, steps);
     return ok ? 0 : 1;
 }

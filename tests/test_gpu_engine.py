@@ -35,3 +35,11 @@ def test_chunked_prompt_crosses_chunk_boundaries():
     reference's attn_long test covers), 4B heads, two layers, then decode steps."""
     rc, res = _run(2, 32, 8, 300, 128, 12, 400)
     assert rc == 0 and res["ok"], res
+
+
+def test_long_prompt_in_512_chunks_then_decode():
+    """A 4000-token prompt in 512-token chunks (the reference engine's chunk cap,
+    src/cuda/model_cuda.cu:1912): later chunks sit at positions up to 3584, where the engine's
+    prefill splits each query block's key range over workgroups; then decode steps at ctx ~4000."""
+    rc, res = _run(1, 32, 8, 4000, 512, 8, 4100)
+    assert rc == 0 and res["ok"], res
