@@ -529,13 +529,9 @@ template <int G, int NW>
 static hipError_t launch_gw(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused) {
     const dim3 grid(a.nsplit, a.HKV, n_seq);
     const size_t lds = (size_t)kRingTiles * kTileFloats * sizeof(float);  // 128 KB
-    static bool opted[2] = {false, false};
-    if (!opted[fused]) {
-        const void* f = fused ? (const void*)k_decode<G, true, NW> : (const void*)k_decode<G, false, NW>;
-        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        opted[fused] = true;
-    }
+    static std::atomic<bool> opted[2];
+    const void* f = fused ? (const void*)k_decode<G, true, NW> : (const void*)k_decode<G, false, NW>;
+    if (const hipError_t e = opt_in_lds(opted[fused], f, lds); e != hipSuccess) return e;
     if (fused) k_decode<G, true, NW><<<grid, 64 * NW, lds, st>>>(a);
     else k_decode<G, false, NW><<<grid, 64 * NW, lds, st>>>(a);
     if (a.nsplit > 1) k_combine<G><<<n_seq * a.H, 128, 0, st>>>(a);

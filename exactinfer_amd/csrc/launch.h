@@ -3,10 +3,20 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 
 namespace ei {
+
+// Opt kernel f into `bytes` of dynamic LDS (> 64 KB needs it) once per process.  Setting the
+// attribute is idempotent, so first launches racing from several host threads only repeat it.
+inline hipError_t opt_in_lds(std::atomic<bool>& done, const void* f, size_t bytes) {
+    if (done.load(std::memory_order_acquire)) return hipSuccess;
+    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess) done.store(true, std::memory_order_release);
+    return e;
+}
 
 // ------------------------------------------------------------------ prologue.hip
 hipError_t launch_headnorm_rope(hipStream_t st, float* buf, int rows, long row_stride, int n_heads,

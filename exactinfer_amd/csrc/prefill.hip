@@ -452,18 +452,10 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
     }
     const size_t lds = (size_t)kKS * kGroupF * sizeof(float);  // > 64 KB: opt in once per instantiation
     static_assert(kKS * kGroupF >= 2 * 4 * kXchF * 64, "merge exchange must fit in the tile buffers");
-    static bool opted[3] = {false, false, false};
+    static std::atomic<bool> opted[3];
     const int oi = GW == 1 ? 0 : GW == 2 ? 1 : 2;
-    if (!opted[oi]) {
-        hipError_t e = GW == 1   ? hipFuncSetAttribute((const void*)k_prefill<1>,
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)
-                       : GW == 2 ? hipFuncSetAttribute((const void*)k_prefill<2>,
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)
-                                 : hipFuncSetAttribute((const void*)k_prefill<4>,
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        opted[oi] = true;
-    }
+    const void* f = GW == 1 ? (const void*)k_prefill<1> : GW == 2 ? (const void*)k_prefill<2> : (const void*)k_prefill<4>;
+    if (const hipError_t e = opt_in_lds(opted[oi], f, lds); e != hipSuccess) return e;
     switch (GW) {
         case 1:
             k_prefill<1><<<grid, 64 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale, ksplit,
