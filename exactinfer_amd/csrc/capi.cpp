@@ -50,8 +50,7 @@ int check_heads(int n_head, int n_head_kv, int head_dim) {
     REQUIRE(n_head > 0 && n_head_kv > 0, "n_head (%d) and n_head_kv (%d) must be positive", n_head, n_head_kv);
     REQUIRE(n_head % n_head_kv == 0, "n_head %d is not a multiple of n_head_kv %d", n_head, n_head_kv);
     const int g = n_head / n_head_kv;
-    if (g != 1 && g != 2 && g != 4 && g != 8)
-        return fail(EI_ERR_UNSUPPORTED, "GQA group %d: built for 1, 2, 4, 8", g);
+    if (g > 8) return fail(EI_ERR_UNSUPPORTED, "GQA group %d: built for groups of 1 to 8 query heads", g);
     return EI_OK;
 }
 
@@ -147,7 +146,7 @@ int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void
     REQUIRE(ws_bytes >= need, "workspace of %zu bytes < %zu needed (ei_attn_decode_ws_bytes)", ws_bytes, need);
     const ei::DecodePlan p = ei::decode_plan(n_seq, a.HKV, max_kv, a.block_table != nullptr);
     const size_t slots = (size_t)n_seq * a.HKV * p.nsplit;
-    const int G = a.H / a.HKV;
+    const int G = ei::decode_group_slots(a.H / a.HKV);  // partials are laid out with the kernel's head slots
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     char* base = static_cast<char*>(ws);
     a.part_acc = reinterpret_cast<float*>(base);

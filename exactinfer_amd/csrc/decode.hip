@@ -180,7 +180,8 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     const int t_end = min(len, t_begin + a.chunk);
     const int pos = len > 0 ? len - 1 : 0;  // a zero-length sequence has no new row; keep the table index valid
     const float* qrow = a.q + (size_t)seq * a.q_stride;
-    const int h0 = kvh * G;
+    const int Gr = a.H / a.HKV;  // heads of this KV head (<= G; heads Gr..G-1 are padding)
+    const int h0 = kvh * Gr;
     float* wring = ring + w * (kRing * kTileFloats);
 
 
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
         const uint32_t qa = __builtin_amdgcn_readfirstlane(lds_addr(qs));
 #pragma unroll
         for (int i = 0; i < (G * D * 4 + 1023) / 1024; ++i)
-            dma_block(qrow + (size_t)h0 * D + 256 * i, qa + 1024 * i, G * D * 4 - 1024 * i, lane);
+            if (1024 * i < Gr * D * 4) dma_block(qrow + (size_t)h0 * D + 256 * i, qa + 1024 * i, Gr * D * 4 - 1024 * i, lane);
         if constexpr (FUSED) {
             dma_block(a.q_gamma, __builtin_amdgcn_readfirstlane(lds_addr(stage)), D * 4, lane);
             dma_block(reinterpret_cast<const float*>(a.cs + (size_t)pos * (a.rope_dim >> 1)),
@@ -230,11 +231,13 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
         else if (ntiles0 >= 1) wait_vmcnt<kTile>();
         else wait_vmcnt<0>();
     }
+    if (G > Gr)  // padding heads: zero queries (finite scores, never written out)
+        for (int i = Gr * D + tid; i < G * D; i += kThreads) qs[i] = 0.f;
     __syncthreads();
 
     if constexpr (FUSED) {
         const float2* cs_row = reinterpret_cast<const float2*>(stage + 2 * D);
-        for (int g = w; g < G; g += kWaves) {  // in place: raw q -> normed, roped q
+        for (int g = w; g < Gr; g += kWaves) {  // in place: raw q -> normed, roped q
             float o0, o1;
             norm_rope_head(qs + g * D, stage, cs_row, a.rope_dim, a.eps, qs + g * D, lane, &o0, &o1);
             qs[g * D + lane] = o0;
@@ -404,7 +407,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     }
 
     if (S == 1) {  // a single split is already the answer
-        if (tid < NCOL) {
+        if (tid < NCOL && gcol < Gr) {
             if (Lw > 0.f) {
                 o.x /= Lw;
                 o.y /= Lw;
@@ -418,7 +421,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
 
     // unnormalised partial of this split; k_combine merges the splits in a second launch
     // (the kernel boundary makes these plain stores visible to every XCD)
-    if (tid < NCOL) {
+    if (tid < NCOL && gcol < Gr) {
         *reinterpret_cast<float4*>(a.part_acc + (slot * G + gcol) * D + 4 * d4) = o;
         if (d4 == 0) *reinterpret_cast<float2*>(a.part_ml + (slot * G + gcol) * 2) = make_float2(Mw, Lw);
     }
@@ -433,7 +436,8 @@ __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
     __shared__ float wsh[kDecodeMaxSplits];
     __shared__ float Lsh;
     const int hq = blockIdx.x % a.H, seq = blockIdx.x / a.H;
-    const int kvh = hq / G, g = hq % G;
+    const int Gr = a.H / a.HKV;  // partials are laid out with G (>= Gr) head slots
+    const int kvh = hq / Gr, g = hq % Gr;
     const int S = a.nsplit, tid = threadIdx.x;
     const size_t head_slot = (size_t)seq * a.HKV + kvh;
     const float* pml = a.part_ml + (head_slot * S * G + g) * 2;
@@ -521,7 +525,7 @@ size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv) {
     const DecodePlan p0 = decode_plan(n_seq, HKV, max_kv, false), p1 = decode_plan(n_seq, HKV, max_kv, true);
     const DecodePlan p = p0.nsplit >= p1.nsplit ? p0 : p1;
     const size_t slots = (size_t)n_seq * HKV * p.nsplit;
-    const int G = H / HKV;
+    const int G = decode_group_slots(H / HKV);
     return align256(slots * G * kHeadDim * 4) + align256(slots * G * 2 * 4);
 }
 
@@ -544,8 +548,11 @@ static hipError_t launch_g(hipStream_t st, const DecodeArgs& a, int n_seq, bool 
     return a.chunk <= 8 * kTile ? launch_gw<G, 8>(st, a, n_seq, fused) : launch_gw<G, 4>(st, a, n_seq, fused);
 }
 
+int decode_group_slots(int g) { return g <= 1 ? 1 : g <= 2 ? 2 : g <= 4 ? 4 : g <= 8 ? 8 : 0; }
+
 hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused) {
-    switch (a.H / a.HKV) {
+    // any group of 1..8 heads runs on the next kernel built for 1, 2, 4 or 8 heads
+    switch (decode_group_slots(a.H / a.HKV)) {
         case 1: return launch_g<1>(st, a, n_seq, fused);
         case 2: return launch_g<2>(st, a, n_seq, fused);
         case 4: return launch_g<4>(st, a, n_seq, fused);

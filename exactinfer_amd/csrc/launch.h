@@ -40,6 +40,7 @@ constexpr int kDecodeMaxSplits = 256;
 constexpr int kDecodePagedMaxChunk = 4096;  // 4 waves x 64 tiles of 16 keys
 DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged);
 size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv);
+int decode_group_slots(int g);  // heads per KV head the decode kernel is built for (0: unsupported)
 
 struct DecodeArgs {
     const float* q;         // raw [Q|K|V] row (fused) or normed q [H][128], per sequence

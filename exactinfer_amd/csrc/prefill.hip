@@ -16,8 +16,14 @@
 // Output block db (0..3) of O^T holds d = 4*i + db for accumulator row i, so the A operand
 // of all four blocks for one key is a single 16-byte LDS read V[key][4*lane .. 4*lane+3].
 //
-// Workgroup = KS key groups x GW query heads (the GW heads of one KV head that share every
-// K/V tile).  Key group g takes the tiles kt = KS*i + g of the block's causal range and
+// Workgroup = KS key groups x 4 query slots of one KV head.  A slot is one (query block,
+// head) pair; slots are numbered s = qb*G + g over the G heads that share the KV head, and
+// unit U of a KV head holds slots 4U..4U+3.  For G = 4 a unit is the four heads of one
+// block, for G = 8 half of them, for G = 2 two heads of two neighbouring blocks, for G = 1
+// four neighbouring blocks of the head, for odd G at most two neighbouring blocks: every
+// wave of the unit shares every K/V tile, and the unit's key range ends at its last
+// block's diagonal (a wave of an earlier block masks the few tiles past its own).  Slots
+// past the last block are idle waves (zero queries, no output).  Key group g takes the tiles kt = KS*i + g of the block's causal range and
 // keeps its own (m, l, O); the groups merge through LDS at the end of the block.  With
 // KS = 2 every SIMD runs two waves whose matrix streams interleave, each covering the
 // other's LDS waits and per-tile softmax preamble.  Inside a wave's stream the next score
@@ -42,8 +48,8 @@
 // softmax (the common factor cancels in O / l).  The causal mask is applied only on the
 // (at most two) tiles that cross the block's diagonal.
 //
-// Causal balance: query block qb needs qb+1+pos0/32 tiles, so a workgroup runs block p
-// and then block nb-1-p; every workgroup has the same amount of work.  Workgroup id
+// Causal balance: unit U needs about (4U+4)/G + pos0/32 tiles, so a workgroup runs unit p
+// and then unit nu-1-p; every workgroup has the same amount of work.  Workgroup id
 // L -> kv head L % HKV first, so with 8 KV heads all blocks of one KV head share an
 // XCD (and its L2) under the round-robin XCD dispatch.
 #include "common.h"
@@ -63,29 +69,29 @@ constexpr int kKS = 2;                           // key groups per workgroup
 constexpr float kLazy = 8.f;                     // lazy-rescale threshold (log2 units)
 constexpr int kXchF = 34;                        // floats per lane exchanged by the merge
 
-template <int GW>
-__global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restrict__ q, long q_stride,
+constexpr int kSlots = 4;                        // query slots (waves) per key group
+
+__global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __restrict__ q, long q_stride,
                                                            float* __restrict__ out, const float* __restrict__ kc,
                                                            const float* __restrict__ vc,
                                                            const int* __restrict__ pos_dev, int B, int H, int HKV,
-                                                           int GG, float scale, int ksplit,
+                                                           float scale, int ksplit,
                                                            float* __restrict__ part_o, float* __restrict__ part_ml) {
     constexpr int D = kHeadDim;
+    constexpr int GW = kSlots;
     constexpr int DMA_PER_WAVE = 16 / GW;  // V DMA instructions per wave per tile (K: twice as many, 32 lanes each)
     extern __shared__ __align__(16) float smem[];
 
     const int L = blockIdx.x;
     const int kvh = L % HKV;
     const int rest = L / HKV;
-    const int hg = rest % GG;
-    const int split = (rest / GG) % ksplit;  // which contiguous share of each block's key tiles
-    const int pair = (rest / GG) / ksplit;
-    const int G = GW * GG;
+    const int split = rest % ksplit;  // which contiguous share of each unit's key tiles
+    const int pair = rest / ksplit;
+    const int G = H / HKV;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wu = __builtin_amdgcn_readfirstlane(w);  // wave-uniform: keeps the branches scalar
     const int hw = wu % GW, grp = wu / GW;
     const int col = lane & 31, hh = lane >> 5;
-    const int h = kvh * G + hg * GW + hw;
     const int pos0 = *pos_dev;
     const size_t KD = (size_t)HKV * D;
     const float* kbase = kc + (size_t)kvh * D;
@@ -95,15 +101,19 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
     const uint32_t voff_k = 16u * col;                                  // K: lanes 0..31, one row
     const uint32_t voff_v = (uint32_t)hh * row_bytes + 16u * col;        // V: two rows per instruction
     const int nb = (B + kQB - 1) / kQB;
+    const int nslot = G * nb;                    // (block, head) slots of this KV head
+    const int nu = (nslot + kSlots - 1) / kSlots;  // units
     float* gsm = smem + grp * kGroupF;  // this key group's buffers: K0 K1 V0 V1
     float* gsv = gsm + 2 * kKTileF;
     const float sl2 = scale * 1.44269504088896340736f;
 
-    // Q^T operand of query block qb: qreg[4*k4 + j] = q[qb*32 + col][h][8*k4 + 4*hh + j]
+    // Q^T operand of this wave's slot of unit u: qreg[4*k4 + j] = q[qb*32 + col][h][8*k4 + 4*hh + j]
     float qreg[64];
-    auto load_q = [&](int qb) {
-        const int b = qb * kQB + col;
-        if (b < B) {
+    auto load_q = [&](int u) {
+        const int sl = kSlots * u + hw;
+        const int b = sl / G * kQB + col;
+        const int h = kvh * G + sl % G;
+        if (sl < nslot && b < B) {
             const float* src = q + (size_t)b * q_stride + (size_t)h * D + 4 * hh;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -118,12 +128,16 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
             for (int i = 0; i < 64; ++i) qreg[i] = 0.f;
         }
     };
-    const int qb_second = nb - 1 - pair;  // the pass-1 block (none when it equals pair)
+    const int u_second = nu - 1 - pair;  // the pass-1 unit (none when it equals pair)
     load_q(pair);
 
     for (int pass = 0; pass < 2; ++pass) {
-        const int qb = pass == 0 ? pair : qb_second;
-        if (pass == 1 && qb == pair) break;
+        const int u = pass == 0 ? pair : u_second;
+        if (pass == 1 && u == pair) break;
+        const int sl = kSlots * u + hw;            // this wave's slot (wave-uniform)
+        const bool live = sl < nslot;
+        const int qb = sl / G, h = kvh * G + sl % G;
+        const int qb_last = min(kSlots * u + kSlots - 1, nslot - 1) / G;  // the unit's last block
         const int b = qb * kQB + col;  // this lane's query row
         const int qpos = pos0 + b;
 
@@ -134,9 +148,9 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
             for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
         float m = -INFINITY, lsum = 0.f;
 
-        const int T = pos0 + min(B, qb * kQB + kQB);   // keys seen by the block's last query
+        const int T = pos0 + min(B, qb_last * kQB + kQB);  // keys seen by the unit's last query
         const int ntile = (T + kKT - 1) / kKT;
-        const int nfull = (pos0 + qb * kQB + 1) / kKT;  // tiles below the diagonal (no mask)
+        const int nfull = live ? (pos0 + qb * kQB + 1) / kKT : ntile;  // tiles below this wave's diagonal
         const int kt_lo = split * ntile / ksplit;       // this workgroup's tiles: [kt_lo, kt_hi)
         const int nrange = (split + 1) * ntile / ksplit - kt_lo;
         const int n_it = (nrange + kKS - 1) / kKS;
@@ -319,7 +333,7 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         }
 
         // the next block's q loads fly during the merge (qreg is dead after the key loop)
-        if (pass == 0 && qb_second != pair) load_q(qb_second);
+        if (pass == 0 && u_second != pair) load_q(u_second);
 
         // ---- merge the key groups through LDS (tile buffers are free after the barrier):
         // group g finalises output blocks db = 2g, 2g+1 and hands the other two to its partner
@@ -341,7 +355,7 @@ __global__ __launch_bounds__(64 * GW * kKS) void k_prefill(const float* __restri
         const float c0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mt);
         const float cp = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - mt);
         const float l = half_sum(lsum * c0 + lp * cp);
-        if (b < B) {
+        if (live && b < B) {
             // O^T register r of block db is d = 4*(8(r/4) + 4hh + r%4) + db
             const size_t rowh = (size_t)b * H + h;
             if (ksplit == 1) {
@@ -405,25 +419,28 @@ __global__ __launch_bounds__(128) void k_prefill_combine(const float* __restrict
 
 static int prefill_grid1(int B, int H, int HKV) {
     const int G = H / HKV;
-    const int GG = G / (G < 4 ? G : 4);
     const int nb = (B + kQB - 1) / kQB;
-    return ((nb + 1) / 2) * HKV * GG;
+    const int nu = (G * nb + kSlots - 1) / kSlots;
+    return ((nu + 1) / 2) * HKV;
 }
 
 int prefill_split(int B, int H, int HKV, int max_kv) {
-    // One workgroup per (query-block pair, KV head) fills the chip only for long chunks.  A
-    // chunk with fewer workgroups than CUs splits every block's key tiles into ksplit
-    // contiguous shares, as many as bring the grid to about one workgroup per CU while
-    // each share keeps >= 4 tiles on average (max_kv bounds pos0 + B on the host, which
-    // does not see the device-resident position).
+    // One workgroup per (unit pair, KV head), all with the same work, one per CU at a time
+    // (128 KB of LDS): the launch takes ceil(g1 / 256) rounds.  Splitting every unit's key
+    // tiles into k contiguous shares makes g1*k workgroups of 1/k the work, so the time goes
+    // as ceil(g1*k / 256) / k.  The plan takes the k in 1..8 with the shortest time, a larger
+    // k only when it gains >= 10% (each share adds a combine read and write), and keeps >= 4
+    // tiles per share on average (max_kv bounds pos0 + B on the host, which does not see the
+    // device-resident position).
     const int g1 = prefill_grid1(B, H, HKV);
-    if (g1 >= 256) return 1;
     const long avg_tiles = ((long)max_kv - B / 2 + kKT - 1) / kKT;
-    int k = (256 + g1 - 1) / g1;
-    const long cap = avg_tiles / 4 > 1 ? avg_tiles / 4 : 1;
-    if (k > cap) k = (int)cap;
-    if (k > kPrefillMaxSplit) k = kPrefillMaxSplit;
-    return k < 1 ? 1 : k;
+    long kmax = avg_tiles / 4 > 1 ? avg_tiles / 4 : 1;
+    if (kmax > kPrefillMaxSplit) kmax = kPrefillMaxSplit;
+    auto rounds = [&](long k) { return (double)((g1 * k + 255) / 256) / (double)k; };
+    int best = 1;
+    for (int k = 2; k <= kmax; ++k)
+        if (rounds(k) < 0.9 * rounds(best)) best = k;
+    return best;
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -438,9 +455,6 @@ size_t prefill_ws_bytes(int B, int H, int HKV, int max_kv) {
 hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
                           const float* vc, const int* pos_dev, int B, int H, int HKV, float scale, int ksplit,
                           void* ws) {
-    const int G = H / HKV;
-    const int GW = G < 4 ? G : 4;
-    const int GG = G / GW;
     if (ksplit < 1) ksplit = 1;
     const unsigned grid = (unsigned)prefill_grid1(B, H, HKV) * ksplit;
     float* part_o = nullptr;
@@ -450,27 +464,12 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
         part_o = static_cast<float*>(ws);
         part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256((size_t)ksplit * rows * kHeadDim * 4));
     }
-    const size_t lds = (size_t)kKS * kGroupF * sizeof(float);  // > 64 KB: opt in once per instantiation
-    static_assert(kKS * kGroupF >= 2 * 4 * kXchF * 64, "merge exchange must fit in the tile buffers");
-    static std::atomic<bool> opted[3];
-    const int oi = GW == 1 ? 0 : GW == 2 ? 1 : 2;
-    const void* f = GW == 1 ? (const void*)k_prefill<1> : GW == 2 ? (const void*)k_prefill<2> : (const void*)k_prefill<4>;
-    if (const hipError_t e = opt_in_lds(opted[oi], f, lds); e != hipSuccess) return e;
-    switch (GW) {
-        case 1:
-            k_prefill<1><<<grid, 64 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale, ksplit,
-                                                      part_o, part_ml);
-            break;
-        case 2:
-            k_prefill<2><<<grid, 128 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale,
-                                                       ksplit, part_o, part_ml);
-            break;
-        case 4:
-            k_prefill<4><<<grid, 256 * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, GG, scale,
-                                                       ksplit, part_o, part_ml);
-            break;
-        default: return hipErrorInvalidValue;
-    }
+    const size_t lds = (size_t)kKS * kGroupF * sizeof(float);  // > 64 KB: opt in once
+    static_assert(kKS * kGroupF >= 2 * kSlots * kXchF * 64, "merge exchange must fit in the tile buffers");
+    static std::atomic<bool> opted{false};
+    if (const hipError_t e = opt_in_lds(opted, (const void*)k_prefill, lds); e != hipSuccess) return e;
+    k_prefill<<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale, ksplit, part_o,
+                                                    part_ml);
     if (ksplit > 1) {
         const int rows = B * H;
         k_prefill_combine<<<(rows + 3) / 4, 128, 0, st>>>(part_o, part_ml, out, rows, ksplit);

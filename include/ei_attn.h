@@ -14,7 +14,8 @@
  *    unchanged while the position advances (src/cuda/model_cuda.cu:1632, :1846).
  *  - fp32 everywhere; head_dim must be 128 (the reference GPU path requires it,
  *    src/cuda/model_cuda.cu:46, :1542); n_head must be a multiple of n_head_kv with a
- *    group size of 1, 2, 4 or 8; rope_dim even and <= head_dim.
+ *    group size of 1 to 8 (every dense Qwen3: 0.6B-8B and 32B have 2, 4 or 8, 14B has 5);
+ *    rope_dim even and <= head_dim.
  *  - KV cache layout per layer: [position][n_head_kv][head_dim] fp32 (src/model.cpp:153,
  *    src/cuda/model_cuda.cu:1571), i.e. row p holds kd = n_head_kv*128 floats.
  *  - Base pointers and row strides must be 16-byte aligned (multiples of 4 floats).
@@ -148,9 +149,10 @@ int ei_attn_prefill(ei_stream_t stream, const float* q, long q_stride, float* ou
 
 /* Key-split prefill for short chunks at long positions.  The reference engine feeds a prompt
  * in chunks of at most 512 tokens (src/cuda/model_cuda.cu:1912) and runs one
- * k_attn_prefill64 per chunk; at 512 tokens one workgroup per query-block pair and KV head
- * leaves most CUs idle.  This variant splits every query block's key range over up to 8
- * workgroups (planned from B and max_kv, an upper bound of *pos_dev + B) and merges the
+ * k_attn_prefill64 per chunk; at 512 tokens (or with GQA groups under 4 heads at any
+ * length) one workgroup per query-block pair and KV head leaves CUs idle.  This variant
+ * splits every query block's key range over up to 8 workgroups, as many as fill whole
+ * rounds of the CUs (planned from B and max_kv, an upper bound of *pos_dev + B) and merges the
  * shares with a second launch, using `ws`: ei_attn_prefill_ws_bytes(max_B, ...) bytes serve
  * every chunk of up to max_B rows (0 bytes when no split is planned; the call then equals
  * ei_attn_prefill).  Same semantics and arguments as ei_attn_prefill otherwise; no

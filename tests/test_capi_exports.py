@@ -43,8 +43,8 @@ def test_argument_errors_are_reported_not_thrown():
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     with pytest.raises(_capi.EiError, match="head_dim 64"):
         _capi.call("ei_attn_prefill", None, p, 4096, p, p, p, p, 8, 32, 8, 64, 0.1)
-    with pytest.raises(_capi.EiError, match="GQA group 3"):
-        _capi.call("ei_attn_prefill", None, p, 4096, p, p, p, p, 8, 24, 8, 128, 0.1)
+    with pytest.raises(_capi.EiError, match="GQA group 16"):
+        _capi.call("ei_attn_prefill", None, p, 4096, p, p, p, p, 8, 128, 8, 128, 0.1)
     with pytest.raises(_capi.EiError, match="multiple of n_head_kv"):
         _capi.call("ei_attn_decode", None, p, p, p, p, p, 30, 8, 128, 0.1, 10, p, 1 << 20)
     with pytest.raises(_capi.EiError, match="workspace"):

@@ -75,7 +75,7 @@ def _hip_attention(model, A, torch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n_head,n_head_kv", [(4, 2), (8, 2)])
+@pytest.mark.parametrize("n_head,n_head_kv", [(4, 2), (8, 2), (10, 2)])
 def test_e2e_logprob_hip_vs_reference(orc, gpu, n_head, n_head_kv):
     import torch
     model = TinyQwen3(seed=11, n_head=n_head, n_head_kv=n_head_kv)

@@ -121,7 +121,8 @@ def _cache(orc, n, HKV, seed, spike_every=0):
 
 @pytest.mark.parametrize("H,HKV,T", [(16, 8, 1), (16, 8, 2), (32, 8, 63), (32, 8, 64), (32, 8, 65), (16, 8, 1000),
                                      (32, 8, 4096), (8, 8, 333), (64, 8, 700), (4, 2, 64), (8, 2, 300),
-                                     (16, 4, 129), (4, 1, 77), (8, 1, 2048)])
+                                     (16, 4, 129), (4, 1, 77), (8, 1, 2048),
+                                     (40, 8, 1000), (12, 4, 300), (6, 1, 129), (7, 1, 64), (40, 8, 4096)])
 def test_decode_matches_reference_attention(orc, gpu, H, HKV, T):
     shape = gpu.AttnShape(H, HKV)
     k, v = _cache(orc, T + 5, HKV, 40 + T)
@@ -183,7 +184,8 @@ def test_decode_batched_ragged(orc, gpu, nseq, empty):
         assert not np.any(out[i]), f"sequence {i} of length 0 is not zeros"
 
 
-@pytest.mark.parametrize("H,HKV,T", [(32, 8, 1), (32, 8, 4096), (16, 8, 777), (4, 2, 55), (8, 1, 300)])
+@pytest.mark.parametrize("H,HKV,T", [(32, 8, 1), (32, 8, 4096), (16, 8, 777), (4, 2, 55), (8, 1, 300), (40, 8, 777),
+                                     (12, 4, 55)])
 def test_fused_decode_step(orc, gpu, H, HKV, T):
     """ei_decode_step == headnorm_rope(Q,K) + append + reference attention, bit-exact cache."""
     shape = gpu.AttnShape(H, HKV)
@@ -210,7 +212,11 @@ def test_fused_decode_step(orc, gpu, H, HKV, T):
 @pytest.mark.parametrize("H,HKV,B,pos0", [(16, 8, 1, 0), (16, 8, 31, 0), (32, 8, 33, 0), (16, 8, 100, 37),
                                           (32, 8, 512, 0), (16, 8, 512, 512), (32, 8, 65, 1000), (64, 8, 40, 3),
                                           (4, 2, 16, 32), (8, 2, 48, 0), (16, 4, 70, 5), (4, 4, 20, 3),
-                                          (8, 1, 97, 200)])
+                                          (8, 1, 97, 200),
+                                          # groups of 5, 3, 7, 1 and 2 heads: units spanning two blocks, idle
+                                          # slots after the last block, ragged last blocks
+                                          (40, 8, 100, 37), (40, 8, 512, 0), (12, 4, 70, 5), (7, 1, 33, 0),
+                                          (8, 8, 200, 0), (8, 8, 129, 64), (16, 8, 70, 0), (16, 8, 97, 300)])
 def test_prefill_matches_reference_attention(orc, gpu, H, HKV, B, pos0):
     shape = gpu.AttnShape(H, HKV)
     n = pos0 + B
@@ -311,7 +317,8 @@ def test_prefill_graph_replays(orc, gpu):
 @pytest.mark.gpu
 @pytest.mark.parametrize("H,HKV,B,pos0,max_kv", [(32, 8, 512, 1536, 2048), (16, 8, 100, 3000, 4096),
                                                  (8, 2, 64, 500, 1024), (32, 8, 33, 0, 4096),
-                                                 (4, 1, 256, 7000, 8192), (64, 8, 40, 900, 1024)])
+                                                 (4, 1, 256, 7000, 8192), (64, 8, 40, 900, 1024),
+                                                 (40, 8, 100, 2000, 4096), (8, 8, 64, 1000, 2048)])
 def test_prefill_split_matches_reference_attention(orc, gpu, H, HKV, B, pos0, max_kv):
     """ei_attn_prefill_split == the reference per-token attention; (32, 8, 33, 0, 4096) plans
     more shares than the chunk has tiles, so empty shares are merged too."""
