@@ -49,7 +49,8 @@ def parse():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the parity-case shapes reported beside the headline (configs[3], configs[4] contiguous "
                          "and paged, configs[2] in 512-token chunks)")
-    ap.add_argument("--only", choices=["decode", "prefill", "prefill-chunked", "longctx", "batched", "batched-paged"],
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill-chunked", "prefill-groups", "longctx", "batched",
+                                         "batched-paged"],
                     default=None)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
@@ -359,6 +360,12 @@ def main():
         res["prefill_chunked"] = bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512)
         log(json.dumps(res["prefill_chunked"]))
         log(json.dumps(bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512, split=False)))
+    if args.only == "prefill-groups":  # GQA group sizes of the dense Qwen3 family, T = 2048 in one chunk
+        res["prefill_groups"] = {}
+        for H, HKV in ((16, 8), (32, 8), (40, 8), (64, 8), (8, 8)):
+            r = bench_prefill_chunked(torch, A, H, HKV, 8, 2048, 2048, seed=2200 + H)
+            res["prefill_groups"][f"H{H}/HKV{HKV}"] = r
+            log(f"H{H}/HKV{HKV}: " + json.dumps(r))
     if extra or args.only == "longctx":
         log("long-context decode configs[3] ...")
         res["longctx"] = bench_decode(torch, A, 16, 8, 28, 32768, max(8, args.steps // 8), 3, use_graph,
@@ -408,7 +415,7 @@ def main():
                            "roofline": {"bound": "mfma", "achieved": round(pre["kernel_tflops"], 3),
                                         "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                                         "frac": round(pre["kernel_tflops"] / FP32_MFMA_PEAK_TFLOPS, 4),
-                                        "traffic": TRAFFIC_PREFILL, "kernel": "k_prefill<4>",
+                                        "traffic": TRAFFIC_PREFILL, "kernel": "k_prefill",
                                         "kernel_us": round(pre["kernel_ms"] * 1e3, 2),
                                         "flops_per_launch": pre["flops_per_launch"]}}
     # the other configs (parity-test shapes), measured beside the headline for context
