@@ -11,8 +11,7 @@
 //     O^T[d][query] = V^T . P^T          (A = V from LDS)
 // because the accumulator row order (8*(r/4) + 4*(lane/32) + r%4) is used as the
 // contraction order of the second product.  In the first product, step 4*k4 + j of lane
-// half hh contracts d = 8*k4 + 4*hh + j: the two halves of a wave read neighbouring 16-byte
-// pieces of each query row, so one q load instruction touches 32 cache lines, not 64.
+// half hh contracts d = 8*k4 + 4*hh + j.
 // Output block db (0..3) of O^T holds d = 4*i + db for accumulator row i, so the A operand
 // of all four blocks for one key is a single 16-byte LDS read V[key][4*lane .. 4*lane+3].
 //
@@ -41,6 +40,12 @@
 //     from many rows runs ~3.5x slower per CU than contiguous DMA);
 //   V tile row-major    [32 keys][128 floats], two rows per 64-lane DMA instruction.
 // Rows past the causal end are clamped to the last visible row (valid memory, masked out).
+// q and the output pass through LDS too, so that global memory sees whole 512-byte rows:
+// at the start of each unit the workgroup DMAs its 128 query rows (once, for both key
+// groups) into a padded staging area and each wave reads its Q^T operand from there; at the
+// end the finished rows are written there in row order and stored two rows per instruction.
+// (Gathering q straight into registers, 32 bytes per row per instruction, twice, and storing
+// 8-byte pieces of 32 rows per instruction held each pass up for several microseconds.)
 //
 // Softmax runs in the exp2 domain (scores x scale x log2 e, one FMA per score).  The
 // running maximum is raised only when a tile's maximum exceeds it by more than kLazy
@@ -68,8 +73,21 @@ constexpr int kGroupF = 2 * kKTileF + 2 * kVTileF;  // per key group: 2 K + 2 V 
 constexpr int kKS = 2;                           // key groups per workgroup
 constexpr float kLazy = 8.f;                     // lazy-rescale threshold (log2 units)
 constexpr int kXchF = 34;                        // floats per lane exchanged by the merge
-
 constexpr int kSlots = 4;                        // query slots (waves) per key group
+
+// n / d for small d (1..8) and n * d < 2^32 as one multiply-high: the per-pass index math
+// runs on the scalar unit, which the eight waves of a CU share, so a division loop per use
+// would cost thousands of cycles per pass.  m = ceil(2^32 / d); d = 1 is taken as is.
+struct FastDiv {
+    uint32_t m, d;
+};
+__device__ __forceinline__ FastDiv fast_div(uint32_t d) { return {d == 1 ? 0u : 0xFFFFFFFFu / d + 1u, d}; }
+__device__ __forceinline__ int fdiv(int n, FastDiv f) {
+    return f.d == 1 ? n : (int)__umulhi((uint32_t)n, f.m);
+}
+// q staging: the unit's 4 x 32 query rows, padded like K rows, after the merge exchange area
+constexpr int kQStageF = 2 * kSlots * kXchF * 64;
+constexpr int kLdsF = kQStageF + kSlots * kQB * kKS_F > kKS * kGroupF ? kQStageF + kSlots * kQB * kKS_F : kKS * kGroupF;
 
 __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __restrict__ q, long q_stride,
                                                            float* __restrict__ out, const float* __restrict__ kc,
@@ -88,6 +106,7 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
     const int split = rest % ksplit;  // which contiguous share of each unit's key tiles
     const int pair = rest / ksplit;
     const int G = H / HKV;
+    const FastDiv fG = fast_div((uint32_t)G), fK = fast_div((uint32_t)ksplit);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wu = __builtin_amdgcn_readfirstlane(w);  // wave-uniform: keeps the branches scalar
     const int hw = wu % GW, grp = wu / GW;
@@ -107,37 +126,53 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
     float* gsv = gsm + 2 * kKTileF;
     const float sl2 = scale * 1.44269504088896340736f;
 
-    // Q^T operand of this wave's slot of unit u: qreg[4*k4 + j] = q[qb*32 + col][h][8*k4 + 4*hh + j]
-    float qreg[64];
-    auto load_q = [&](int u) {
-        const int sl = kSlots * u + hw;
-        const int b = sl / G * kQB + col;
-        const int h = kvh * G + sl % G;
-        if (sl < nslot && b < B) {
-            const float* src = q + (size_t)b * q_stride + (size_t)h * D + 4 * hh;
+    // q of unit u reaches LDS by LDS DMA, once per workgroup: row r = 32*slot + j holds query
+    // qb*32 + j of the slot's head (one contiguous 512-byte DMA per row; rows past B and idle
+    // slots are clamped to valid rows, never written out).  Both key groups then read their
+    // Q^T operand from it: qreg[4*k4 + j] = q[qb*32 + col][h][8*k4 + 4*hh + j].
+    float* qst = smem + kQStageF;
+    auto stage_q = [&](int u) {
+        // wave wu stages rows 16*wu .. 16*wu+15: half of slot wu/2 (scalar work is shared by the
+        // CU's eight waves, so the per-row address step is one add)
+        const int sl = kSlots * u + (wu >> 1);
+        const int qsl = fdiv(sl, fG);
+        const int qbs = sl < nslot ? qsl : nb - 1;
+        const int r0 = min(qbs * kQB + (kQB / 2) * (wu & 1), B - 1);
+        const int jm = B - 1 - r0;  // rows past B repeat the last row
+        uint64_t sb = (uint64_t)(uintptr_t)(q + (size_t)r0 * q_stride + (size_t)(kvh * G + sl - qsl * G) * D);
+        const uint32_t rs = (uint32_t)(q_stride * sizeof(float));
+        const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(qst + (kQB / 2) * wu * kKS_F));
+        if (hh == 0) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float4 v = *reinterpret_cast<const float4*>(src + 8 * i);
-                qreg[4 * i] = v.x;
-                qreg[4 * i + 1] = v.y;
-                qreg[4 * i + 2] = v.z;
-                qreg[4 * i + 3] = v.w;
+            for (int j = 0; j < kQB / 2; ++j) {
+                dma16_s(sb, voff_k, lb + j * (kKS_F * 4));
+                if (j < jm) sb += rs;
             }
-        } else {
+        }
+    };
+    float qreg[64];
+    auto read_q = [&]() {
+        wait_vmcnt<0>();
+        __syncthreads();
+        const float* qs = qst + (hw * kQB + col) * kKS_F + 4 * hh;
 #pragma unroll
-            for (int i = 0; i < 64; ++i) qreg[i] = 0.f;
+        for (int i = 0; i < 16; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(qs + 8 * i);
+            qreg[4 * i] = v.x;
+            qreg[4 * i + 1] = v.y;
+            qreg[4 * i + 2] = v.z;
+            qreg[4 * i + 3] = v.w;
         }
     };
     const int u_second = nu - 1 - pair;  // the pass-1 unit (none when it equals pair)
-    load_q(pair);
 
     for (int pass = 0; pass < 2; ++pass) {
         const int u = pass == 0 ? pair : u_second;
         if (pass == 1 && u == pair) break;
         const int sl = kSlots * u + hw;            // this wave's slot (wave-uniform)
         const bool live = sl < nslot;
-        const int qb = sl / G, h = kvh * G + sl % G;
-        const int qb_last = min(kSlots * u + kSlots - 1, nslot - 1) / G;  // the unit's last block
+        const int qb = fdiv(sl, fG), h = kvh * G + sl - qb * G;
+        const int qb_last = fdiv(min(kSlots * u + kSlots - 1, nslot - 1), fG);  // the unit's last block
         const int b = qb * kQB + col;  // this lane's query row
         const int qpos = pos0 + b;
 
@@ -151,8 +186,8 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         const int T = pos0 + min(B, qb_last * kQB + kQB);  // keys seen by the unit's last query
         const int ntile = (T + kKT - 1) / kKT;
         const int nfull = live ? (pos0 + qb * kQB + 1) / kKT : ntile;  // tiles below this wave's diagonal
-        const int kt_lo = split * ntile / ksplit;       // this workgroup's tiles: [kt_lo, kt_hi)
-        const int nrange = (split + 1) * ntile / ksplit - kt_lo;
+        const int kt_lo = fdiv(split * ntile, fK);       // this workgroup's tiles: [kt_lo, kt_hi)
+        const int nrange = fdiv((split + 1) * ntile, fK) - kt_lo;
         const int n_it = (nrange + kKS - 1) / kKS;
         const int n_mine = (nrange - grp + kKS - 1) / kKS;  // tiles of this key group
 
@@ -301,7 +336,10 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         // i: DMA K(i+2) -> K[i%2] and V(i+1) -> V[(i+1)%2] (both last read in iteration
         // i-1), read K(i+1) and V(i) (both landed by the wait + barrier ending i-1).
         // The score tiles alternate between sa and sb (loop unrolled by two).
-        __syncthreads();  // previous pass (or merge) finished with every buffer
+        if (pass > 0) __syncthreads();  // every wave has stored its rows from the staging area
+        stage_q(u);
+        read_q();
+        __syncthreads();  // every wave has its q (the staging area is reused by the tile buffers)
         if (n_mine > 0) {
             dma_k(0, 0);
             dma_v(0, 0);
@@ -332,9 +370,6 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
             if (i + 1 < n_it) iter(i + 1, sb, sa);
         }
 
-        // the next block's q loads fly during the merge (qreg is dead after the key loop)
-        if (pass == 0 && u_second != pair) load_q(u_second);
-
         // ---- merge the key groups through LDS (tile buffers are free after the barrier):
         // group g finalises output blocks db = 2g, 2g+1 and hands the other two to its partner
         float* xw = smem + w * (kXchF * 64) + lane;
@@ -355,31 +390,35 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         const float c0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mt);
         const float cp = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - mt);
         const float l = half_sum(lsum * c0 + lp * cp);
-        if (live && b < B) {
-            // O^T register r of block db is d = 4*(8(r/4) + 4hh + r%4) + db
-            const size_t rowh = (size_t)b * H + h;
-            if (ksplit == 1) {
-                const float inv = 1.f / l;
-                float* dst = out + rowh * D + 16 * hh + 2 * grp;
+        // finished rows (normalised, or the unnormalised share for k_prefill_combine) go to the
+        // staging area in row order, then every wave stores two whole 512-byte rows per instruction
+        {
+            const float inv = ksplit == 1 ? 1.f / l : 1.f;
+            float* ost = qst + (hw * kQB + col) * kKS_F + 2 * grp;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float2 v;
-                    v.x = (keep0[r] * c0 + xp[(2 + r) * 64] * cp) * inv;
-                    v.y = (keep1[r] * c0 + xp[(18 + r) * 64] * cp) * inv;
-                    *reinterpret_cast<float2*>(dst + 4 * (8 * (r >> 2) + (r & 3))) = v;
-                }
-            } else {
-                // unnormalised share (m in log2 units, l, O) for k_prefill_combine
-                const size_t slot = (size_t)split * B * H + rowh;
-                float* dst = part_o + slot * D + 16 * hh + 2 * grp;
+            for (int r = 0; r < 16; ++r) {
+                // O^T register r of block db is d = 4*(8(r/4) + 4hh + r%4) + db
+                float2 v;
+                v.x = (keep0[r] * c0 + xp[(2 + r) * 64] * cp) * inv;
+                v.y = (keep1[r] * c0 + xp[(18 + r) * 64] * cp) * inv;
+                *reinterpret_cast<float2*>(ost + 4 * (8 * (r >> 2) + 4 * hh + (r & 3))) = v;
+            }
+            if (ksplit > 1 && live && b < B && hh == 0 && grp == 0)
+                *reinterpret_cast<float2*>(part_ml + ((size_t)split * B * H + (size_t)b * H + h) * 2) =
+                    make_float2(mt, l);
+        }
+        __syncthreads();
+        {
+            const int sl = kSlots * u + (wu >> 1);  // wave wu stores rows 16*(wu&1).. of slot wu/2
+            const int qbo = fdiv(sl, fG), ho = kvh * G + sl - qbo * G;
+            float* dst0 = ksplit == 1 ? out : part_o + (size_t)split * B * H * D;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float2 v;
-                    v.x = keep0[r] * c0 + xp[(2 + r) * 64] * cp;
-                    v.y = keep1[r] * c0 + xp[(18 + r) * 64] * cp;
-                    *reinterpret_cast<float2*>(dst + 4 * (8 * (r >> 2) + (r & 3))) = v;
-                }
-                if (hh == 0 && grp == 0) *reinterpret_cast<float2*>(part_ml + slot * 2) = make_float2(mt, l);
+            for (int j = 0; j < kQB / 4; ++j) {
+                const int jj = (kQB / 2) * (wu & 1) + 2 * j + hh;
+                const int bo = qbo * kQB + jj;
+                const float4 v = *reinterpret_cast<const float4*>(qst + ((wu >> 1) * kQB + jj) * kKS_F + 4 * col);
+                if (sl < nslot && bo < B)
+                    *reinterpret_cast<float4*>(dst0 + ((size_t)bo * H + ho) * D + 4 * col) = v;
             }
         }
     }
@@ -464,8 +503,9 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
         part_o = static_cast<float*>(ws);
         part_ml = reinterpret_cast<float*>(static_cast<char*>(ws) + align256((size_t)ksplit * rows * kHeadDim * 4));
     }
-    const size_t lds = (size_t)kKS * kGroupF * sizeof(float);  // > 64 KB: opt in once
+    const size_t lds = (size_t)kLdsF * sizeof(float);  // > 64 KB: opt in once
     static_assert(kKS * kGroupF >= 2 * kSlots * kXchF * 64, "merge exchange must fit in the tile buffers");
+    static_assert(kLdsF * sizeof(float) <= 160 * 1024, "LDS budget");
     static std::atomic<bool> opted{false};
     if (const hipError_t e = opt_in_lds(opted, (const void*)k_prefill, lds); e != hipSuccess) return e;
     k_prefill<<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale, ksplit, part_o,
