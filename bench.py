@@ -49,8 +49,8 @@ def parse():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the parity-case shapes reported beside the headline (configs[3], configs[4] contiguous "
                          "and paged, configs[2] in 512-token chunks)")
-    ap.add_argument("--only", choices=["decode", "prefill", "prefill-chunked", "prefill-groups", "longctx", "batched",
-                                         "batched-paged"],
+    ap.add_argument("--only", choices=["decode", "decode-groups", "prefill", "prefill-chunked", "prefill-groups", "longctx",
+                                         "batched", "batched-paged"],
                     default=None)
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
@@ -360,6 +360,12 @@ def main():
         res["prefill_chunked"] = bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512)
         log(json.dumps(res["prefill_chunked"]))
         log(json.dumps(bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512, split=False)))
+    if args.only == "decode-groups":  # configs[1]'s decode at the other dense Qwen3 group sizes
+        res["decode_groups"] = {}
+        for H, HKV in ((16, 8), (32, 8), (40, 8), (64, 8)):
+            r = bench_decode(torch, A, H, HKV, 36, 4096, args.steps, args.warmup, use_graph, seed=5000 + H)
+            res["decode_groups"][f"H{H}/HKV{HKV}"] = r
+            log(f"H{H}/HKV{HKV}: " + json.dumps(r))
     if args.only == "prefill-groups":  # GQA group sizes of the dense Qwen3 family, T = 2048 in one chunk
         res["prefill_groups"] = {}
         for H, HKV in ((16, 8), (32, 8), (40, 8), (64, 8), (8, 8)):

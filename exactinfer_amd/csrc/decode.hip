@@ -256,11 +256,20 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
         }
     }
 
-    float4 qreg[G][4];
+    // q operand of the score phase: held in registers for up to 4 heads; 8 heads would take 128
+    // VGPRs, so they are read from the LDS copy at each use (the 8 lanes of a chunk read one
+    // address: broadcast reads)
+    constexpr bool kQInRegs = G <= 2;
+    float4 qreg[kQInRegs ? G : 1][4];
+    if constexpr (kQInRegs)
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qreg[g][i] = *reinterpret_cast<const float4*>(qs + g * D + 4 * c + 32 * i);
+            for (int i = 0; i < 4; ++i) qreg[g][i] = *reinterpret_cast<const float4*>(qs + g * D + 4 * c + 32 * i);
+    auto qv = [&](int g, int i) -> float4 {
+        if constexpr (kQInRegs) return qreg[g][i];
+        else return *reinterpret_cast<const float4*>(qs + g * D + 4 * c + 32 * i);
+    };
 
     float m[G];         // running max per head (wave-uniform)
     float l[NF];        // per-lane partial denominators of this lane's (row, head) slots
@@ -302,7 +311,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
             for (int i = 0; i < 4; ++i) {
                 const float4 kv = *reinterpret_cast<const float4*>(tk + tile_off(8 * j + r, c + 8 * i));
 #pragma unroll
-                for (int g = 0; g < G; ++g) part[j * G + g] = dot4(qreg[g][i], kv, part[j * G + g]);
+                for (int g = 0; g < G; ++g) part[j * G + g] = dot4(qv(g, i), kv, part[j * G + g]);
             }
         xreduce8<NV>(part, c);
 
@@ -342,7 +351,8 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
             __builtin_amdgcn_wave_barrier();
         }
         const int voff = 2 * (lane & 1);
-#pragma unroll
+        // (8 heads: a partly unrolled loop keeps the row's p values and V pieces within the register budget)
+#pragma unroll(G >= 4 ? 4 : kTile)
         for (int k = 0; k < kTile; ++k) {
             const float2 vv = *reinterpret_cast<const float2*>(tv + tile_off(k, lane >> 1) + voff);
 #pragma unroll
