@@ -20,7 +20,8 @@
 // per-sequence offset (contiguous ranges) or from a block table (paged pools).
 //
 //   scores    lane (r = l/8, c = l%8) reads rows r and r+8 at d = 4c + 32i (i < 4) and
-//             holds q for those d in registers; the 8 lanes of a row hold partial dots for
+//             takes q for those d from registers (G <= 2) or from the workgroup's LDS
+//             copy (more heads: register budget); the 8 lanes of a row hold partial dots for
 //             (2 rows x G heads) and a transposing butterfly over lanes xor 1/2/4 leaves
 //             one finished score per lane (7 exchanges for G = 4).
 //   softmax   the tile max per head is a 4-step butterfly over the lanes holding that
@@ -29,6 +30,9 @@
 //             overlap the transfer of its V rows.
 //   values    lane l owns d = 2l, 2l+1 of all 16 rows and accumulates p * v for the G
 //             heads.
+//
+// Groups of 3, 5, 6 or 7 heads run on the kernel built for the next power of two, with the
+// extra head slots idle (zero queries, never written out).
 //
 // Split combine: each workgroup writes its unnormalised partial (m, l, acc[G][128]); a
 // second, small launch (k_combine, one workgroup per query head) merges them,
