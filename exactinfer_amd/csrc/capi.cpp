@@ -359,6 +359,37 @@ EI_API int ei_attn_prefill_split(ei_stream_t stream, const float* q, long q_stri
                       "prefill launch");
 }
 
+EI_API int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, float* out, float* kc, float* vc,
+                           const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim, const float* q_gamma,
+                           const float* k_gamma, const float* cs, int rope_dim, float eps, float scale, int max_kv,
+                           void* ws, size_t ws_bytes) {
+    if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
+    if (int e = check_rope(rope_dim, head_dim)) return e;
+    REQUIRE(qkv && out && kc && vc && pos_dev && q_gamma && k_gamma && cs, "null pointer argument");
+    REQUIRE(B >= 0, "B %d", B);
+    REQUIRE(max_kv >= B, "max_kv %d < B %d", max_kv, B);
+    REQUIRE(row_stride >= (long)(n_head + 2 * n_head_kv) * head_dim, "row_stride %ld < (H+2*HKV)*head_dim",
+            row_stride);
+    REQUIRE(aligned16(qkv) && aligned16(out) && aligned16(kc) && aligned16(vc) && row_stride % 4 == 0,
+            "pointers and row_stride must be 16-byte aligned");
+    if (B == 0) return ok();
+    const int ksplit = ei::prefill_split(B, n_head, n_head_kv, max_kv);
+    const size_t need = ei::prefill_ws_bytes(B, n_head, n_head_kv, max_kv);
+    REQUIRE(ws_bytes >= need, "workspace %zu B < %zu B (ei_attn_prefill_ws_bytes)", ws_bytes, need);
+    REQUIRE(need == 0 || (ws && aligned16(ws)), "workspace must be a 16-byte aligned device pointer");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    // the attention kernel norms q itself for the full-width RoPE (Qwen3); any other rope_dim
+    // takes the prologue for every head and the plain kernel
+    const bool fuse_q = rope_dim == head_dim;
+    if (int e = hip_status(ei::launch_qkv_prepare(st, qkv, B, row_stride, n_head, n_head_kv, q_gamma, k_gamma, cs,
+                                                  pos_dev, rope_dim, eps, kc, vc, fuse_q ? n_head : 0),
+                           "prefill step: prologue launch"))
+        return e;
+    return hip_status(ei::launch_prefill(st, qkv, row_stride, out, kc, vc, pos_dev, B, n_head, n_head_kv, scale, ksplit,
+                                         ws, fuse_q ? q_gamma : nullptr, cs, rope_dim, eps),
+                      "prefill step: attention launch");
+}
+
 EI_API int ei_synth_fill(ei_stream_t stream, float* dst, size_t n, uint64_t seed, uint64_t offset, long row_len,
                          long spike_every, float spike_mult) {
     REQUIRE(dst != nullptr || n == 0, "dst is null");

@@ -23,9 +23,10 @@ hipError_t launch_headnorm_rope(hipStream_t st, float* buf, int rows, long row_s
                                 const float* gamma, const float* cs, const int* pos_dev, int rope_dim, float eps);
 hipError_t launch_kv_append(hipStream_t st, const float* k_src, const float* v_src, long src_stride, int rows,
                             float* kc, float* vc, int kd, const int* pos_dev);
+// h_begin: first head processed (0: all; H: the key heads and the cache append only)
 hipError_t launch_qkv_prepare(hipStream_t st, float* qkv, int rows, long row_stride, int H, int HKV,
                               const float* q_gamma, const float* k_gamma, const float* cs, const int* pos_dev,
-                              int rope_dim, float eps, float* kc, float* vc);
+                              int rope_dim, float eps, float* kc, float* vc, int h_begin = 0);
 hipError_t launch_synth_fill(hipStream_t st, float* dst, size_t n, uint64_t seed, uint64_t offset, long row_len,
                              long spike_every, float spike_mult);
 
@@ -76,8 +77,11 @@ hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes);
 constexpr int kPrefillMaxSplit = 8;
 int prefill_split(int B, int H, int HKV, int max_kv);
 size_t prefill_ws_bytes(int B, int H, int HKV, int max_kv);  // 0 when no split is planned
+// q_gamma != nullptr: the q rows are raw projections; the kernel applies QK-norm + RoPE (table
+// cs, eps; rope_dim must be 128) to each row where it stages it, leaving the q buffer untouched.
 hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
                           const float* vc, const int* pos_dev, int B, int H, int HKV, float scale, int ksplit,
-                          void* ws);
+                          void* ws, const float* q_gamma = nullptr, const float* cs = nullptr, int rope_dim = 0,
+                          float eps = 0.f);
 
 }  // namespace ei

@@ -89,12 +89,59 @@ __device__ __forceinline__ int fdiv(int n, FastDiv f) {
 constexpr int kQStageF = 2 * kSlots * kXchF * 64;
 constexpr int kLdsF = kQStageF + kSlots * kQB * kKS_F > kKS * kGroupF ? kQStageF + kSlots * kQB * kKS_F : kKS * kGroupF;
 
+// QK-norm + RoPE of one q row in LDS (rope_dim = 128), eight lanes per row: lane k of the row
+// holds elements 8k..8k+7 and their rotate-half partners 64+8k..64+8k+7.  Same arithmetic as the
+// prologue's head-norm (the reference's k_headnorm_rope, src/cuda/model_cuda.cu:87-105): sum of
+// squares in double, inv = float(1/sqrt(ss/128 + eps)), y = (x*inv)*gamma, then
+// (y_e, y_e+64) -> (y_e c - y_e+64 s, y_e s + y_e+64 c).  The double sum runs over the eight
+// lanes' partial sums (a different order of exact products than the prologue's lane pairs; the
+// float result is the same unless the double rounds across a float boundary).
+__device__ __forceinline__ void norm_rope_q8(float* row, const float (&g)[16], const float4 (&t)[4], float eps,
+                                             int k) {
+#pragma clang fp contract(off)
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float4 a = *reinterpret_cast<const float4*>(row + 8 * k + 4 * i);
+        const float4 b = *reinterpret_cast<const float4*>(row + 64 + 8 * k + 4 * i);
+        x[4 * i] = a.x, x[4 * i + 1] = a.y, x[4 * i + 2] = a.z, x[4 * i + 3] = a.w;
+        x[8 + 4 * i] = b.x, x[8 + 4 * i + 1] = b.y, x[8 + 4 * i + 2] = b.z, x[8 + 4 * i + 3] = b.w;
+    }
+    // float x float is exact in double, so fma(x, x, ss) rounds like ss + x*x
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ss = __builtin_fma((double)x[i], (double)x[i], ss);
+    ss += lane_xor_f64<1>(ss);
+    ss += lane_xor_f64<2>(ss);
+    ss += lane_xor_f64<4>(ss);
+    const float inv = (float)(1.0 / sqrt(ss / (double)kHeadDim + (double)eps));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float c = (i & 1) ? t[i >> 1].z : t[i >> 1].x, sn = (i & 1) ? t[i >> 1].w : t[i >> 1].y;
+        const float a = (x[i] * inv) * g[i];
+        const float b = (x[8 + i] * inv) * g[8 + i];
+        const float acs = a * c, bsn = b * sn;
+        const float asn = a * sn, bcs = b * c;
+        x[i] = acs - bsn;
+        x[8 + i] = asn + bcs;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        *reinterpret_cast<float4*>(row + 8 * k + 4 * i) = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+        *reinterpret_cast<float4*>(row + 64 + 8 * k + 4 * i) =
+            make_float4(x[8 + 4 * i], x[8 + 4 * i + 1], x[8 + 4 * i + 2], x[8 + 4 * i + 3]);
+    }
+}
+
+template <bool kNormQ>
 __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __restrict__ q, long q_stride,
                                                            float* __restrict__ out, const float* __restrict__ kc,
                                                            const float* __restrict__ vc,
                                                            const int* __restrict__ pos_dev, int B, int H, int HKV,
                                                            float scale, int ksplit,
-                                                           float* __restrict__ part_o, float* __restrict__ part_ml) {
+                                                           float* __restrict__ part_o, float* __restrict__ part_ml,
+                                                           const float* __restrict__ q_gamma,
+                                                           const float2* __restrict__ cs, int rope_dim, float eps) {
     constexpr int D = kHeadDim;
     constexpr int GW = kSlots;
     constexpr int DMA_PER_WAVE = 16 / GW;  // V DMA instructions per wave per tile (K: twice as many, 32 lanes each)
@@ -131,15 +178,20 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
     // slots are clamped to valid rows, never written out).  Both key groups then read their
     // Q^T operand from it: qreg[4*k4 + j] = q[qb*32 + col][h][8*k4 + 4*hh + j].
     float* qst = smem + kQStageF;
-    auto stage_q = [&](int u) {
-        // wave wu stages rows 16*wu .. 16*wu+15: half of slot wu/2 (scalar work is shared by the
-        // CU's eight waves, so the per-row address step is one add)
+    // wave wu stages rows 16*wu .. 16*wu+15 of unit u: half of slot wu/2, query rows r0 + min(j, jm)
+    auto stage_rows = [&](int u, int& r0, int& jm, int& hq) {
         const int sl = kSlots * u + (wu >> 1);
         const int qsl = fdiv(sl, fG);
         const int qbs = sl < nslot ? qsl : nb - 1;
-        const int r0 = min(qbs * kQB + (kQB / 2) * (wu & 1), B - 1);
-        const int jm = B - 1 - r0;  // rows past B repeat the last row
-        uint64_t sb = (uint64_t)(uintptr_t)(q + (size_t)r0 * q_stride + (size_t)(kvh * G + sl - qsl * G) * D);
+        r0 = min(qbs * kQB + (kQB / 2) * (wu & 1), B - 1);
+        jm = B - 1 - r0;  // rows past B repeat the last row
+        hq = kvh * G + sl - qsl * G;
+    };
+    auto stage_q = [&](int u) {
+        // (scalar work is shared by the CU's eight waves, so the per-row address step is one add)
+        int r0, jm, hq;
+        stage_rows(u, r0, jm, hq);
+        uint64_t sb = (uint64_t)(uintptr_t)(q + (size_t)r0 * q_stride + (size_t)hq * D);
         const uint32_t rs = (uint32_t)(q_stride * sizeof(float));
         const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(qst + (kQB / 2) * wu * kKS_F));
         if (hh == 0) {
@@ -151,8 +203,37 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         }
     };
     float qreg[64];
-    auto read_q = [&]() {
-        wait_vmcnt<0>();
+    auto read_q = [&](int u) {
+        if constexpr (kNormQ) {
+            // raw q rows: QK-norm + RoPE in place, each wave on the 16 rows it staged, 8 lanes per
+            // row, two rounds of 8 rows; gamma and both rounds' RoPE rows are loaded while the
+            // q rows are still in flight
+            int r0, jm, hq;
+            stage_rows(u, r0, jm, hq);
+            const int k = lane & 7, j = lane >> 3;
+            float g[16];
+            float4 t[2][4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float4 ga = *reinterpret_cast<const float4*>(q_gamma + 8 * k + 4 * i);
+                const float4 gb = *reinterpret_cast<const float4*>(q_gamma + 64 + 8 * k + 4 * i);
+                g[4 * i] = ga.x, g[4 * i + 1] = ga.y, g[4 * i + 2] = ga.z, g[4 * i + 3] = ga.w;
+                g[8 + 4 * i] = gb.x, g[8 + 4 * i + 1] = gb.y, g[8 + 4 * i + 2] = gb.z, g[8 + 4 * i + 3] = gb.w;
+            }
+            const int p0 = *pos_dev + r0;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float4* tr = reinterpret_cast<const float4*>(cs + (size_t)(p0 + min(8 * h + j, jm)) * (kHeadDim / 2) + 8 * k);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) t[h][i] = tr[i];
+            }
+            wait_vmcnt<0>();
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                norm_rope_q8(qst + ((kQB / 2) * wu + 8 * h + j) * kKS_F, g, t[h], eps, k);
+        } else {
+            wait_vmcnt<0>();
+        }
         __syncthreads();
         const float* qs = qst + (hw * kQB + col) * kKS_F + 4 * hh;
 #pragma unroll
@@ -338,7 +419,7 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         // The score tiles alternate between sa and sb (loop unrolled by two).
         if (pass > 0) __syncthreads();  // every wave has stored its rows from the staging area
         stage_q(u);
-        read_q();
+        read_q(u);
         __syncthreads();  // every wave has its q (the staging area is reused by the tile buffers)
         if (n_mine > 0) {
             dma_k(0, 0);
@@ -493,7 +574,7 @@ size_t prefill_ws_bytes(int B, int H, int HKV, int max_kv) {
 
 hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
                           const float* vc, const int* pos_dev, int B, int H, int HKV, float scale, int ksplit,
-                          void* ws) {
+                          void* ws, const float* q_gamma, const float* cs, int rope_dim, float eps) {
     if (ksplit < 1) ksplit = 1;
     const unsigned grid = (unsigned)prefill_grid1(B, H, HKV) * ksplit;
     float* part_o = nullptr;
@@ -506,10 +587,17 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
     const size_t lds = (size_t)kLdsF * sizeof(float);  // > 64 KB: opt in once
     static_assert(kKS * kGroupF >= 2 * kSlots * kXchF * 64, "merge exchange must fit in the tile buffers");
     static_assert(kLdsF * sizeof(float) <= 160 * 1024, "LDS budget");
-    static std::atomic<bool> opted{false};
-    if (const hipError_t e = opt_in_lds(opted, (const void*)k_prefill, lds); e != hipSuccess) return e;
-    k_prefill<<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale, ksplit, part_o,
-                                                    part_ml);
+    static std::atomic<bool> opted[2];
+    const bool nq = q_gamma != nullptr;
+    const void* f = nq ? (const void*)k_prefill<true> : (const void*)k_prefill<false>;
+    if (const hipError_t e = opt_in_lds(opted[nq], f, lds); e != hipSuccess) return e;
+    if (nq)
+        k_prefill<true><<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale, ksplit,
+                                                              part_o, part_ml, q_gamma,
+                                                              reinterpret_cast<const float2*>(cs), rope_dim, eps);
+    else
+        k_prefill<false><<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
+                                                               ksplit, part_o, part_ml, nullptr, nullptr, 0, 0.f);
     if (ksplit > 1) {
         const int rows = B * H;
         k_prefill_combine<<<(rows + 3) / 4, 128, 0, st>>>(part_o, part_ml, out, rows, ksplit);

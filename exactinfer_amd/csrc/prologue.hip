@@ -44,18 +44,19 @@ __global__ __launch_bounds__(256) void k_kv_append(const float* __restrict__ k_s
 // row (2 KB) and issues all their loads (and the V rows of its key heads) before any
 // arithmetic, so a wave keeps 8-16 loads in flight.  Head index hh < H: query head
 // (q_gamma); otherwise key head hh-H (k_gamma), whose normed row also goes to the cache
-// together with the raw V row of the same kv head.  src/cuda/model_cuda.cu:1800-1806.
+// together with the raw V row of the same kv head.  Heads below h_begin are skipped (h_begin = H:
+// the keys and the append only, when the prefill normalises q itself).  src/cuda/model_cuda.cu:1800-1806.
 constexpr int kPrepHeads = 4;  // heads per wave
 __global__ __launch_bounds__(256) void k_qkv_prepare(float* __restrict__ qkv, long row_stride, int H, int HKV,
                                                      const float* __restrict__ q_gamma,
                                                      const float* __restrict__ k_gamma,
                                                      const float2* __restrict__ cs, const int* __restrict__ pos_dev,
                                                      int rope_dim, float eps, float* __restrict__ kc,
-                                                     float* __restrict__ vc) {
+                                                     float* __restrict__ vc, int h_begin) {
     __shared__ float scratch[4][kHeadDim];
     const int b = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int NH = H + HKV;
-    const int h0 = (blockIdx.y * 4 + w) * kPrepHeads;
+    const int h0 = h_begin + (blockIdx.y * 4 + w) * kPrepHeads;
     if (h0 >= NH) return;  // wave-uniform; this kernel has no block barrier
     float* row = qkv + (size_t)b * row_stride;
     const int pos = *pos_dev + b;
@@ -125,11 +126,11 @@ hipError_t launch_kv_append(hipStream_t st, const float* k_src, const float* v_s
 
 hipError_t launch_qkv_prepare(hipStream_t st, float* qkv, int rows, long row_stride, int H, int HKV,
                               const float* q_gamma, const float* k_gamma, const float* cs, const int* pos_dev,
-                              int rope_dim, float eps, float* kc, float* vc) {
-    const int groups = (H + HKV + 4 * kPrepHeads - 1) / (4 * kPrepHeads);  // 4 waves x kPrepHeads heads
+                              int rope_dim, float eps, float* kc, float* vc, int h_begin) {
+    const int groups = (H + HKV - h_begin + 4 * kPrepHeads - 1) / (4 * kPrepHeads);  // 4 waves x kPrepHeads heads
     k_qkv_prepare<<<dim3(rows, groups), 256, 0, st>>>(qkv, row_stride, H, HKV, q_gamma, k_gamma,
                                                                   reinterpret_cast<const float2*>(cs), pos_dev,
-                                                                  rope_dim, eps, kc, vc);
+                                                                  rope_dim, eps, kc, vc, h_begin);
     return hipGetLastError();
 }
 

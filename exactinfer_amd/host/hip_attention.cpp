@@ -94,12 +94,10 @@ void HipAttention::layer(int l, float* qkv, long qkv_stride, const float* q_norm
         check(ei_decode_step(stream_, qkv, qkv_stride, att, kcache(l), vcache(l), nullptr, nullptr, pos_dev_, 1, H,
                              HKV, D, q_norm, k_norm, rope_, c_.rope_dim, c_.eps, scale_, n_ctx_, ws_, ws_bytes_));
     } else {
-        // prompt chunk: QK-norm + RoPE + append for all B rows, then causal attention over
-        // cache rows 0..pos0+b (earlier chunks included)
-        check(ei_qkv_prepare(stream_, qkv, B_, qkv_stride, H, HKV, D, q_norm, k_norm, rope_, pos_dev_, c_.rope_dim,
-                             c_.eps, kcache(l), vcache(l)));
-        check(ei_attn_prefill_split(stream_, qkv, qkv_stride, att, kcache(l), vcache(l), pos_dev_, B_, H, HKV, D,
-                                    scale_, n_ctx_, pws_, pws_bytes_));
+        // prompt chunk: QK-norm + RoPE + append of the K rows, then causal attention over cache
+        // rows 0..pos0+b (earlier chunks included) with q normed inside the attention kernel
+        check(ei_prefill_step(stream_, qkv, qkv_stride, att, kcache(l), vcache(l), pos_dev_, B_, H, HKV, D, q_norm,
+                              k_norm, rope_, c_.rope_dim, c_.eps, scale_, n_ctx_, pws_, pws_bytes_));
     }
 }
 

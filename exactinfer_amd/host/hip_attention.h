@@ -53,9 +53,10 @@ public:
     //   qkv [B][(H + 2*HKV)*128] raw projections, row stride qkv_stride floats;
     //   q_norm / k_norm: the layer's attn_q_norm / attn_k_norm weights [128] (device);
     //   att [B][H*128] output (device).
-    // B == 1 runs the fused decode step (qkv is read only); B > 1 normalises Q and K in place,
-    // appends the chunk's K/V and runs the causal fp32-MFMA prefill (key range split over
-    // workgroups when the chunk alone would not fill the GPU).
+    // B == 1 runs the fused decode step (qkv is read only); B > 1 runs the fused prefill step:
+    // K normalised in place and appended with V, causal fp32-MFMA prefill with Q normalised
+    // inside the kernel (key range split over workgroups when the chunk alone would not fill
+    // the GPU).
     void layer(int l, float* qkv, long qkv_stride, const float* q_norm, const float* k_norm, float* att);
 
     // Device views of layer l's cache, [n_ctx][n_head_kv][128] fp32.

@@ -162,6 +162,19 @@ int ei_attn_prefill_split(ei_stream_t stream, const float* q, long q_stride, flo
                           const float* vc, const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim,
                           float scale, int max_kv, void* ws, size_t ws_bytes);
 
+/* Fused prefill step for a chunk of B tokens at positions *pos_dev .. *pos_dev+B-1: the
+ * per-layer sequence k_headnorm_rope(Q), k_headnorm_rope(K), k_store_kv, k_attn_prefill64 of
+ * src/cuda/model_cuda.cu:1800-1820 in two launches (plus the key-split merge when planned).
+ * qkv rows [Q|K|V] are raw projections: the K heads are normed + roped in place and appended
+ * with the V rows to cache rows *pos_dev + b (as ei_qkv_prepare does).  With rope_dim = 128
+ * (every Qwen3) the Q heads are left raw in qkv and normed + roped inside the attention kernel
+ * where it stages them; with a partial rope_dim they are normed in place by the prologue
+ * first.  Same workspace and plan as ei_attn_prefill_split; out [B][n_head][128]. */
+int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, float* out, float* kc, float* vc,
+                    const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim, const float* q_gamma,
+                    const float* k_gamma, const float* cs, int rope_dim, float eps, float scale, int max_kv, void* ws,
+                    size_t ws_bytes);
+
 /* ------------------------------------------------------------------ synthetic inputs
  * Not part of the reference path: fills n floats with the counter-based N(0,1)
  * generator (element e = stream element offset+e of `seed`), multiplying by spike_mult

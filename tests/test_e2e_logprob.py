@@ -4,8 +4,8 @@ The reference quotes max |delta logprob| <= 2.7e-5 against its numpy forward
 (tests/parity_reference.py:35-107, README); that harness needs GGUF weights, which this
 environment lacks.  The same gate is applied here to a random-weight model with Qwen3's block
 structure: one run with the CPU restatement of the reference's attention (src/model.cpp:174-214),
-one with this build's HIP path (prefill chunks through ei_qkv_prepare + ei_attn_prefill, decode
-steps through ei_decode_step), all other arithmetic shared.  The CPU tests check the harness
+one with this build's HIP path (prefill chunks through ei_prefill_step, decode steps through
+ei_decode_step), all other arithmetic shared.  The CPU tests check the harness
 itself: the float32 reference attention sits well inside the gate against a float64 one, and a
 plausible mistake (softmax scale 1/sqrt(127)) falls outside it.
 """
@@ -56,6 +56,7 @@ def _hip_attention(model, A, torch):
         kg = [torch.from_numpy(L["k_norm"]).to(dev) for L in model.layers]
         cs = A.rope_table(n_ctx, device=dev)
         ws = A.DecodeWorkspace(1, H, HKV, n_ctx, device=dev)
+        pws = A.PrefillWorkspace(n_ctx, H, HKV, n_ctx, device=dev)
 
         def attn(l, qkv, pos0):
             n = qkv.shape[0]
@@ -64,8 +65,7 @@ def _hip_attention(model, A, torch):
             if n == 1:
                 out = A.decode_step(t, kc[l], vc[l], shape, qg[l], kg[l], cs, ws, pos_dev=pos)
             else:
-                A.qkv_prepare(t, shape, qg[l], kg[l], cs, pos, kc[l], vc[l])
-                out = A.attn_prefill(t, kc[l], vc[l], pos, shape)
+                out = A.prefill_step(t, kc[l], vc[l], shape, qg[l], kg[l], cs, pos, pws)
             torch.cuda.synchronize()
             return out.cpu().numpy().reshape(n, H * D)
 

@@ -365,6 +365,77 @@ def test_prefill_split_graph_replays_track_position(orc, gpu):
         assert rel_err(_host(out), ref) <= ATTN_RTOL, f"pos0 {p0}"
 
 
+# ---------------------------------------------------------------- fused prefill step (q normed inside the attention kernel)
+@pytest.mark.gpu
+@pytest.mark.parametrize("H,HKV,B,pos0,max_kv,rope_dim", [(32, 8, 100, 37, 256, 128), (16, 8, 512, 1536, 2048, 128),
+                                                          (40, 8, 64, 1000, 2048, 128), (8, 1, 33, 0, 64, 128),
+                                                          (16, 8, 70, 5, 128, 64)])
+def test_prefill_step_matches_reference(orc, gpu, H, HKV, B, pos0, max_kv, rope_dim):
+    """ei_prefill_step == headnorm_rope(Q), headnorm_rope(K), append, reference attention:
+    cache rows and the in-place K heads bit-exact, attention within ATTN_RTOL; the Q heads stay
+    raw in qkv when the kernel norms them itself (rope_dim 128) and are normed in place
+    otherwise (rope_dim 64 takes the prologue for every head)."""
+    shape = gpu.AttnShape(H, HKV, rope_dim=rope_dim)
+    n_ctx = max(max_kv, pos0 + B)
+    k, v = _cache(orc, n_ctx, HKV, 1500 + B)
+    qkv = orc.normal((B, shape.qkv), 1501 + pos0)
+    qg, kg = orc.gamma(D, 5), orc.gamma(D, 6)
+    cs = gpu.rope_table(n_ctx, rope_dim=rope_dim)
+    kc, vc = _dev(k.reshape(n_ctx, -1)), _dev(v.reshape(n_ctx, -1))
+    buf = _dev(qkv)
+    ws = gpu.PrefillWorkspace(B, H, HKV, max_kv)
+    out = _host(gpu.prefill_step(buf, kc, vc, shape, _dev(qg), _dev(kg), cs, _pos(pos0), ws))
+    normed = orc.headnorm_rope(qkv, H, D, qg, pos0, rope_dim, 1e6, 1e-6)
+    normed = orc.headnorm_rope(normed, HKV, D, kg, pos0, rope_dim, 1e6, 1e-6, col0=H * D)
+    rk, rv = k.reshape(n_ctx, -1).copy(), v.reshape(n_ctx, -1).copy()
+    orc.kv_append(normed[:, H * D:(H + HKV) * D], normed[:, (H + HKV) * D:], rk, rv, pos0)
+    assert bits_equal(_host(kc), rk) and bits_equal(_host(vc), rv)
+    got = _host(buf)
+    assert bits_equal(got[:, H * D:], normed[:, H * D:])
+    assert bits_equal(got[:, :H * D], qkv[:, :H * D] if rope_dim == D else normed[:, :H * D])
+    qn = np.ascontiguousarray(normed[:, :H * D])
+    ref = orc.attn_prefill(qn, rk.reshape(n_ctx, HKV, D), rv.reshape(n_ctx, HKV, D), B, pos0, H, HKV, D)
+    exact = None
+    if rel_err(out, ref) > ATTN_RTOL:  # long rows: the reference's sequential fp32 sums drift
+        kk, vv = rk, rv
+        exact = np.stack([orc.attn_f64(qn[b].reshape(H, D), kk, vv, pos0 + b + 1, H, HKV, D) for b in range(B)])
+    ok, msg = attn_parity(out, ref, exact)
+    assert ok, msg
+
+
+@pytest.mark.gpu
+def test_prefill_step_graph_replays(orc, gpu):
+    """One captured fused prefill step replayed at three positions, the raw projections restored
+    before each replay (the step norms the K heads in place); each replay equals the eager call."""
+    import torch
+    H, HKV, B, max_kv = 32, 8, 96, 1024
+    shape = gpu.AttnShape(H, HKV)
+    k, v = _cache(orc, max_kv, HKV, 1600)
+    raw = _dev(orc.normal((B, shape.qkv), 1601))
+    qg, kg = _dev(orc.gamma(D, 7)), _dev(orc.gamma(D, 8))
+    cs = gpu.rope_table(max_kv)
+    kc0, vc0 = _dev(k.reshape(max_kv, -1)), _dev(v.reshape(max_kv, -1))
+    kc, vc, buf = kc0.clone(), vc0.clone(), raw.clone()
+    pos = _pos(0)
+    ws = gpu.PrefillWorkspace(B, H, HKV, max_kv)
+    out = torch.empty((B, H, D), dtype=torch.float32, device="cuda")
+    gpu.prefill_step(buf, kc, vc, shape, qg, kg, cs, pos, ws, out=out)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gpu.prefill_step(buf, kc, vc, shape, qg, kg, cs, pos, ws, out=out)
+    for p0 in (0, 400, max_kv - B):
+        pos.fill_(p0)
+        buf.copy_(raw), kc.copy_(kc0), vc.copy_(vc0)
+        out.zero_()
+        graph.replay()
+        got, got_k = _host(out), _host(kc)
+        buf.copy_(raw), kc.copy_(kc0), vc.copy_(vc0)
+        eager = _host(gpu.prefill_step(buf, kc, vc, shape, qg, kg, cs, pos, ws))
+        assert bits_equal(got, eager), f"pos0 {p0}"
+        assert bits_equal(got_k, _host(kc)), f"pos0 {p0}"
+
+
 # ---------------------------------------------------------------- paged KV (multi-sequence serving)
 def _paged_layout(rng, lens, bs, shared_prefix_blocks, spare=3):
     """Block tables over a shuffled pool: sequences 0 and 1 share their first blocks."""
