@@ -386,7 +386,7 @@ EI_API int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, floa
                            "prefill step: prologue launch"))
         return e;
     return hip_status(ei::launch_prefill(st, qkv, row_stride, out, kc, vc, pos_dev, B, n_head, n_head_kv, scale, ksplit,
-                                         ws, fuse_q ? q_gamma : nullptr, cs, rope_dim, eps),
+                                         ws, fuse_q ? q_gamma : nullptr, cs, eps),
                       "prefill step: attention launch");
 }
 

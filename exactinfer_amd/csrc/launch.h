@@ -77,11 +77,11 @@ hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes);
 constexpr int kPrefillMaxSplit = 8;
 int prefill_split(int B, int H, int HKV, int max_kv);
 size_t prefill_ws_bytes(int B, int H, int HKV, int max_kv);  // 0 when no split is planned
-// q_gamma != nullptr: the q rows are raw projections; the kernel applies QK-norm + RoPE (table
-// cs, eps; rope_dim must be 128) to each row where it stages it, leaving the q buffer untouched.
+// q_gamma != nullptr: the q rows are raw projections; the kernel applies QK-norm + full-width
+// RoPE (table cs of rope_dim 128, eps) to each row where it stages it, leaving the q buffer
+// untouched.
 hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
                           const float* vc, const int* pos_dev, int B, int H, int HKV, float scale, int ksplit,
-                          void* ws, const float* q_gamma = nullptr, const float* cs = nullptr, int rope_dim = 0,
-                          float eps = 0.f);
+                          void* ws, const float* q_gamma = nullptr, const float* cs = nullptr, float eps = 0.f);
 
 }  // namespace ei

@@ -141,7 +141,7 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
                                                            float scale, int ksplit,
                                                            float* __restrict__ part_o, float* __restrict__ part_ml,
                                                            const float* __restrict__ q_gamma,
-                                                           const float2* __restrict__ cs, int rope_dim, float eps) {
+                                                           const float2* __restrict__ cs, float eps) {
     constexpr int D = kHeadDim;
     constexpr int GW = kSlots;
     constexpr int DMA_PER_WAVE = 16 / GW;  // V DMA instructions per wave per tile (K: twice as many, 32 lanes each)
@@ -574,7 +574,7 @@ size_t prefill_ws_bytes(int B, int H, int HKV, int max_kv) {
 
 hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
                           const float* vc, const int* pos_dev, int B, int H, int HKV, float scale, int ksplit,
-                          void* ws, const float* q_gamma, const float* cs, int rope_dim, float eps) {
+                          void* ws, const float* q_gamma, const float* cs, float eps) {
     if (ksplit < 1) ksplit = 1;
     const unsigned grid = (unsigned)prefill_grid1(B, H, HKV) * ksplit;
     float* part_o = nullptr;
@@ -594,10 +594,10 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
     if (nq)
         k_prefill<true><<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale, ksplit,
                                                               part_o, part_ml, q_gamma,
-                                                              reinterpret_cast<const float2*>(cs), rope_dim, eps);
+                                                              reinterpret_cast<const float2*>(cs), eps);
     else
         k_prefill<false><<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
-                                                               ksplit, part_o, part_ml, nullptr, nullptr, 0, 0.f);
+                                                               ksplit, part_o, part_ml, nullptr, nullptr, 0.f);
     if (ksplit > 1) {
         const int rows = B * H;
         k_prefill_combine<<<(rows + 3) / 4, 128, 0, st>>>(part_o, part_ml, out, rows, ksplit);
