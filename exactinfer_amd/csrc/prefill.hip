@@ -546,7 +546,7 @@ static int prefill_grid1(int B, int H, int HKV) {
 
 int prefill_split(int B, int H, int HKV, int max_kv) {
     // One workgroup per (unit pair, KV head), all with the same work, one per CU at a time
-    // (128 KB of LDS): the launch takes ceil(g1 / 256) rounds.  Splitting every unit's key
+    // (134 KB of LDS): the launch takes ceil(g1 / 256) rounds.  Splitting every unit's key
     // tiles into k contiguous shares makes g1*k workgroups of 1/k the work, so the time goes
     // as ceil(g1*k / 256) / k.  The plan takes the k in 1..8 with the shortest time, a larger
     // k only when it gains >= 10% (each share adds a combine read and write), and keeps >= 4
