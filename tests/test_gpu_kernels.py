@@ -122,7 +122,8 @@ def _cache(orc, n, HKV, seed, spike_every=0):
 @pytest.mark.parametrize("H,HKV,T", [(16, 8, 1), (16, 8, 2), (32, 8, 63), (32, 8, 64), (32, 8, 65), (16, 8, 1000),
                                      (32, 8, 4096), (8, 8, 333), (64, 8, 700), (4, 2, 64), (8, 2, 300),
                                      (16, 4, 129), (4, 1, 77), (8, 1, 2048),
-                                     (40, 8, 1000), (12, 4, 300), (6, 1, 129), (7, 1, 64), (40, 8, 4096)])
+                                     (40, 8, 1000), (12, 4, 300), (6, 1, 129), (7, 1, 64), (40, 8, 4096),
+                                     (48, 8, 2000)])
 def test_decode_matches_reference_attention(orc, gpu, H, HKV, T):
     shape = gpu.AttnShape(H, HKV)
     k, v = _cache(orc, T + 5, HKV, 40 + T)
@@ -216,7 +217,8 @@ def test_fused_decode_step(orc, gpu, H, HKV, T):
                                           # groups of 5, 3, 7, 1 and 2 heads: units spanning two blocks, idle
                                           # slots after the last block, ragged last blocks
                                           (40, 8, 100, 37), (40, 8, 512, 0), (12, 4, 70, 5), (7, 1, 33, 0),
-                                          (8, 8, 200, 0), (8, 8, 129, 64), (16, 8, 70, 0), (16, 8, 97, 300)])
+                                          (8, 8, 200, 0), (8, 8, 129, 64), (16, 8, 70, 0), (16, 8, 97, 300),
+                                          (48, 8, 90, 10), (32, 8, 1, 3000)])
 def test_prefill_matches_reference_attention(orc, gpu, H, HKV, B, pos0):
     shape = gpu.AttnShape(H, HKV)
     n = pos0 + B
@@ -318,7 +320,8 @@ def test_prefill_graph_replays(orc, gpu):
 @pytest.mark.parametrize("H,HKV,B,pos0,max_kv", [(32, 8, 512, 1536, 2048), (16, 8, 100, 3000, 4096),
                                                  (8, 2, 64, 500, 1024), (32, 8, 33, 0, 4096),
                                                  (4, 1, 256, 7000, 8192), (64, 8, 40, 900, 1024),
-                                                 (40, 8, 100, 2000, 4096), (8, 8, 64, 1000, 2048)])
+                                                 (40, 8, 100, 2000, 4096), (8, 8, 64, 1000, 2048),
+                                                 (32, 8, 1, 3000, 4096)])
 def test_prefill_split_matches_reference_attention(orc, gpu, H, HKV, B, pos0, max_kv):
     """ei_attn_prefill_split == the reference per-token attention; (32, 8, 33, 0, 4096) plans
     more shares than the chunk has tiles, so empty shares are merged too."""
@@ -369,7 +372,8 @@ def test_prefill_split_graph_replays_track_position(orc, gpu):
 @pytest.mark.gpu
 @pytest.mark.parametrize("H,HKV,B,pos0,max_kv,rope_dim", [(32, 8, 100, 37, 256, 128), (16, 8, 512, 1536, 2048, 128),
                                                           (40, 8, 64, 1000, 2048, 128), (8, 1, 33, 0, 64, 128),
-                                                          (16, 8, 70, 5, 128, 64)])
+                                                          (16, 8, 70, 5, 128, 64), (32, 8, 1, 500, 1024, 128),
+                                                          (48, 8, 40, 100, 512, 128)])
 def test_prefill_step_matches_reference(orc, gpu, H, HKV, B, pos0, max_kv, rope_dim):
     """ei_prefill_step == headnorm_rope(Q), headnorm_rope(K), append, reference attention:
     cache rows and the in-place K heads bit-exact, attention within ATTN_RTOL; the Q heads stay
