@@ -194,15 +194,24 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     // anything before the whole workgroup's 128 KB is in flight
     const int tw0 = t_begin + kTile * w;
     constexpr int kStride = kTile * kWaves;  // distance between a wave's consecutive tiles
-    // paged: lane i holds the cache row of this wave's tile i (the plan keeps <= 64 tiles per
-    // wave), read back with readlane: one table load per wave instead of one per tile
-    int lane_row = 0;
+    // paged: lane i of lane_row holds the cache row of this wave's tile i, lane i of lane_row2
+    // that of tile 64+i (the plan keeps <= 128 tiles per wave), read back with readlane: one or
+    // two table loads per wave instead of one per tile
+    int lane_row = 0, lane_row2 = 0;
     if (btab) {
-        const int t = min(tw0 + lane * kStride, max(t_end - 1, 0));
+        const int tl = max(t_end - 1, 0);
+        const int t = min(tw0 + lane * kStride, tl);
         lane_row = (btab[t >> bshift] << bshift) | (t & bmask);
+        if (tw0 + 64 * kStride < t_end) {
+            const int t2 = min(tw0 + (lane + 64) * kStride, tl);
+            lane_row2 = (btab[t2 >> bshift] << bshift) | (t2 & bmask);
+        }
     }
     auto tile_row = [&](int t0) -> size_t {
-        return btab ? (size_t)(uint32_t)__builtin_amdgcn_readlane(lane_row, (t0 - tw0) / kStride) : (size_t)t0;
+        if (!btab) return (size_t)t0;
+        const int i = (t0 - tw0) / kStride;
+        return (size_t)(uint32_t)(i < 64 ? __builtin_amdgcn_readlane(lane_row, i)
+                                         : __builtin_amdgcn_readlane(lane_row2, i - 64));
     };
     const bool owner = FUSED && t_begin <= pos && pos < t_end;
     if (w == 0) {
@@ -522,7 +531,7 @@ DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged) {
         const int v = std::atoi(env);
         if (v >= 64 && v % 64 == 0) chunk = v;
     }
-    // paged: a wave keeps the cache rows of its tiles in one register (<= 64 tiles, 4 waves)
+    // paged: a wave keeps the cache rows of its tiles in two registers (<= 128 tiles, 4 waves)
     if (paged && chunk > kDecodePagedMaxChunk) chunk = kDecodePagedMaxChunk;
     while (((long)max_kv + chunk - 1) / chunk > kDecodeMaxSplits) chunk *= 2;
     DecodePlan p;

@@ -38,7 +38,7 @@ struct DecodePlan {
     int nsplit;
 };
 constexpr int kDecodeMaxSplits = 256;
-constexpr int kDecodePagedMaxChunk = 4096;  // 4 waves x 64 tiles of 16 keys
+constexpr int kDecodePagedMaxChunk = 8192;  // 4 waves x 128 tiles of 16 keys
 DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged);
 size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv);
 int decode_group_slots(int g);  // heads per KV head the decode kernel is built for (0: unsupported)

@@ -487,6 +487,26 @@ def test_decode_paged_matches_reference(orc, gpu, bs):
         assert rel_err(out[s], ref) <= ATTN_RTOL, f"sequence {s} (len {n})"
 
 
+@pytest.mark.parametrize("bs", [16, 64])
+def test_decode_paged_long_sequences_whole_chunks(orc, gpu, bs):
+    """32 sequences x 8 KV heads = 256 units: the plan runs each (sequence, KV head) as one
+    8192-key chunk, so a wave walks up to 128 tiles and reads the cache rows of tiles 64..127
+    from its second row register."""
+    H, HKV = 8, 8
+    rng = np.random.default_rng(70 + bs)
+    lens = np.concatenate([np.array([8192, 6000, 4097, 5000], np.int32), rng.integers(1, 200, 28).astype(np.int32)])
+    table, nblocks = _paged_layout(rng, lens, bs, 0)
+    pool_k, pool_v = _cache(orc, nblocks * bs, HKV, 5000 + bs)
+    q = orc.normal((len(lens), H * D), 5001)
+    shape = gpu.AttnShape(H, HKV)
+    ws = gpu.DecodeWorkspace(len(lens), H, HKV, max_kv=8192)
+    out = _host(gpu.attn_decode_paged(_dev(q), _dev(pool_k), _dev(pool_v), _dev(table), bs, _dev(lens), shape, ws))
+    for s_, n in enumerate(lens):
+        kk, vv = _gather(pool_k, table, s_, n, bs), _gather(pool_v, table, s_, n, bs)
+        ref = orc.attn_decode(q[s_].reshape(H, D), kk, vv, int(n), H, HKV, D)
+        assert rel_err(out[s_], ref) <= ATTN_RTOL, f"sequence {s_} (len {n})"
+
+
 def test_decode_step_paged_appends_to_physical_rows(orc, gpu):
     """Fused paged step: each sequence's new K/V row lands in its physical row (bit-exact),
     the shared prefix blocks and every other row stay untouched, attention sees the append."""
