@@ -87,6 +87,27 @@ def test_prefill_split_workspace_contract():
         _capi.call("ei_attn_prefill_split", None, p, 4096, p, p, p, p, 512, 32, 8, 128, 0.1, 100, p, 1 << 30)
 
 
+def test_prefill_step_argument_errors():
+    from exactinfer_amd import _capi
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    args = dict(row_stride=6144, B=512, H=32, HKV=8, D=128, rope_dim=128, max_kv=2048, ws_bytes=1 << 30)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return _capi.call("ei_prefill_step", None, p, a["row_stride"], p, p, p, p, a["B"], a["H"], a["HKV"], a["D"],
+                          p, p, p, a["rope_dim"], 1e-6, 0.1, a["max_kv"], p, a["ws_bytes"])
+    with pytest.raises(_capi.EiError, match="rope_dim 130"):
+        call(rope_dim=130)
+    with pytest.raises(_capi.EiError, match="row_stride"):
+        call(row_stride=4096)
+    with pytest.raises(_capi.EiError, match="max_kv"):
+        call(max_kv=100)
+    with pytest.raises(_capi.EiError, match="workspace"):
+        call(ws_bytes=16)
+    with pytest.raises(_capi.EiError, match="GQA group 16"):
+        call(H=128)
+
+
 def test_paged_argument_errors():
     from exactinfer_amd import _capi
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
