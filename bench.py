@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 Qwen3 attention hot path (one GPU).
 
-Default workload: Qwen3-4B-shape decode attention, batch 1,
+Default workload (the headline metric's configs[1]): Qwen3-4B-shape decode attention, batch 1,
 32 query heads / 8 KV heads / head_dim 128, 36 layers each with its own fp32 KV cache of
 4096 positions.  One step = one new token through all 36 layers: per layer one fused
 launch (QK-norm + RoPE of Q and K, KV append at position 4095, split-K attention over

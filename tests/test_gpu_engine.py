@@ -23,7 +23,7 @@ def _run(*args):
 
 
 def test_config0_prefill512_decode128():
-    """0.6B heads (16/8), one layer, 512-token prefill then 128 decode
+    """configs[0] of the benchmark definition: 0.6B heads (16/8), one layer, 512-token prefill then 128 decode
     steps, each appending to the KV cache."""
     rc, res = _run(1, 16, 8, 512, 512, 128, 640)
     assert rc == 0 and res["ok"], res
