@@ -31,6 +31,15 @@ HipAttention::HipAttention(const AttnConfig& cfg, int n_ctx, int max_batch, hipS
     // scale as the reference computes it (src/model.cpp:163, src/cuda/model_cuda.cu:1786)
     scale_ = 1.0f / std::sqrt(float(c_.head_dim));
 
+    try {
+        allocate();
+    } catch (...) {
+        release();  // the destructor does not run for a constructor that throws
+        throw;
+    }
+}
+
+void HipAttention::allocate() {
     const size_t kd = size_t(c_.n_head_kv) * c_.head_dim;
     const size_t per_cache = size_t(c_.n_layer) * size_t(n_ctx_) * kd * sizeof(float);
     hip_check(hipMalloc(&kv_, 2 * per_cache), "KV cache");
@@ -54,7 +63,9 @@ HipAttention::HipAttention(const AttnConfig& cfg, int n_ctx, int max_batch, hipS
     hip_check(hipStreamSynchronize(stream_), "init");
 }
 
-HipAttention::~HipAttention() {
+HipAttention::~HipAttention() { release(); }
+
+void HipAttention::release() noexcept {
     if (stream_) (void)hipStreamSynchronize(stream_);
     if (pos_host_) (void)hipHostFree(pos_host_);
     if (pos_dev_) (void)hipFree(pos_dev_);
@@ -62,6 +73,10 @@ HipAttention::~HipAttention() {
     if (pws_) (void)hipFree(pws_);
     if (rope_) (void)hipFree(rope_);
     if (kv_) (void)hipFree(kv_);
+    pos_host_ = nullptr;
+    pos_dev_ = nullptr;
+    ws_ = pws_ = nullptr;
+    rope_ = kv_ = nullptr;
 }
 
 void HipAttention::begin_chunk(int pos0, int B) {

@@ -65,6 +65,8 @@ public:
 
 private:
     void check(int status) const;
+    void allocate();
+    void release() noexcept;
 
     AttnConfig c_;
     int n_ctx_, max_batch_;
