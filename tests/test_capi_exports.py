@@ -80,6 +80,13 @@ def test_prefill_split_workspace_contract():
     assert L.ei_attn_prefill_ws_bytes(0, 32, 8, 2048) == 0
     assert L.ei_attn_prefill_ws_bytes(512, 30, 8, 2048) == 0
     assert L.ei_attn_prefill_ws_bytes(512, 32, 8, 100) == 0  # max_kv < max_B
+    # one 2048-token chunk: G = 4 fills the CUs unsplit (256 workgroups); G = 2 gives half as many
+    # workgroups, so the plan splits its keys (a workspace is needed even at max_B = 2048 alone)
+    rows = lambda B, H: B * H
+    g4 = L.ei_attn_prefill_ws_bytes(2048, 32, 8, 2048)
+    g2 = L.ei_attn_prefill_ws_bytes(2048, 16, 8, 2048)
+    assert g2 >= 2 * rows(2048, 16) * 128 * 4  # at least two shares of every (row, head)
+    assert g4 > 0  # smaller chunks up to 2048 split
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     with pytest.raises(_capi.EiError, match="workspace"):
         _capi.call("ei_attn_prefill_split", None, p, 4096, p, p, p, p, 512, 32, 8, 128, 0.1, 2048, p, 16)
