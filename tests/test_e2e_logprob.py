@@ -88,6 +88,22 @@ def test_e2e_logprob_hip_vs_reference(orc, gpu, n_head, n_head_kv):
 
 
 @pytest.mark.gpu
+def test_e2e_logprob_longer_prompt(orc, gpu):
+    """Four layers, a 320-token prompt in chunks of 128, 128 and 64 (the later chunks at pos0 > 0
+    take key-split prefill shares through ei_prefill_step), then 24 decode steps at contexts
+    past 320: the same gate."""
+    import torch
+    model = TinyQwen3(seed=31, n_layer=4, n_head=8, n_head_kv=2)
+    chunks, n_decode, n_ctx = [128, 128, 64], 24, 512
+    toks = np.random.default_rng(32).integers(0, model.V, size=sum(chunks) + n_decode + 1)
+    ref = run_sequence(model, oracle_attention(model, orc), toks, chunks, n_decode, n_ctx)
+    hip = run_sequence(model, _hip_attention(model, gpu, torch), toks, chunks, n_decode, n_ctx)
+    d = float(np.max(np.abs(hip - ref)))
+    print(f"e2e long: max |d logprob| = {d:.3e} over {len(ref)} positions", flush=True)
+    assert d <= LOGPROB_TOL, f"max |delta logprob| {d:.2e} > {LOGPROB_TOL}"
+
+
+@pytest.mark.gpu
 def test_serve_prefix_reuse_equals_generate(orc, gpu):
     """The reference's serve invariant (tests/serve_test.py): a persistent server reusing the
     KV rows of a cached common prefix produces the same greedy tokens as a fresh generate, on
