@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void k_kv_append(const float* __restrict__ k_s
 // (q_gamma); otherwise key head hh-H (k_gamma), whose normed row also goes to the cache
 // together with the raw V row of the same kv head.  Heads below h_begin are skipped (h_begin = H:
 // the keys and the append only, when the prefill normalises q itself).  src/cuda/model_cuda.cu:1800-1806.
-constexpr int kPrepHeads = 4;  // heads per wave
+template <int kPrepHeads>  // heads per wave: 4 for all heads, 2 for the key heads alone (every wave busy)
 __global__ __launch_bounds__(256) void k_qkv_prepare(float* __restrict__ qkv, long row_stride, int H, int HKV,
                                                      const float* __restrict__ q_gamma,
                                                      const float* __restrict__ k_gamma,
@@ -127,10 +127,15 @@ hipError_t launch_kv_append(hipStream_t st, const float* k_src, const float* v_s
 hipError_t launch_qkv_prepare(hipStream_t st, float* qkv, int rows, long row_stride, int H, int HKV,
                               const float* q_gamma, const float* k_gamma, const float* cs, const int* pos_dev,
                               int rope_dim, float eps, float* kc, float* vc, int h_begin) {
-    const int groups = (H + HKV - h_begin + 4 * kPrepHeads - 1) / (4 * kPrepHeads);  // 4 waves x kPrepHeads heads
-    k_qkv_prepare<<<dim3(rows, groups), 256, 0, st>>>(qkv, row_stride, H, HKV, q_gamma, k_gamma,
-                                                                  reinterpret_cast<const float2*>(cs), pos_dev,
-                                                                  rope_dim, eps, kc, vc, h_begin);
+    const int nh = H + HKV - h_begin;
+    const float2* cs2 = reinterpret_cast<const float2*>(cs);
+    if (nh <= 8) {  // 4 waves x 2 heads
+        k_qkv_prepare<2><<<dim3(rows, (nh + 7) / 8), 256, 0, st>>>(qkv, row_stride, H, HKV, q_gamma, k_gamma, cs2,
+                                                                     pos_dev, rope_dim, eps, kc, vc, h_begin);
+    } else {  // 4 waves x 4 heads
+        k_qkv_prepare<4><<<dim3(rows, (nh + 15) / 16), 256, 0, st>>>(qkv, row_stride, H, HKV, q_gamma, k_gamma, cs2,
+                                                                       pos_dev, rope_dim, eps, kc, vc, h_begin);
+    }
     return hipGetLastError();
 }
 
