@@ -279,9 +279,11 @@ def bench_prefill(torch, A, H, HKV, n_layer, T, steps, warmup, seed=2000):
             "kernel_tflops": flops_layer / (kern_ms * 1e-3) / 1e12, "flops_per_launch": flops_layer}
 
 
-def bench_prefill_chunked(torch, A, H, HKV, n_layer, T, chunk, split=True, seed=2100):
+def bench_prefill_chunked(torch, A, H, HKV, n_layer, T, chunk, split=True, seed=2100, step=False):
     """configs[2]'s prompt as the reference engine feeds it: chunks of `chunk` tokens at pos0 = 0, chunk, ...
-    (src/cuda/model_cuda.cu:1912 caps a prefill chunk at 512).  Attention launches only, one graph."""
+    (src/cuda/model_cuda.cu:1912 caps a prefill chunk at 512).  Attention launches only, one graph; with
+    step=True the engine's whole chunk path instead (ei_prefill_step: key prologue + attention with q normed
+    in-kernel; replays re-norm the K heads in place, which keeps them bounded)."""
     shape = A.AttnShape(H, HKV)
     dev = "cuda"
     kd = HKV * D
@@ -292,16 +294,23 @@ def bench_prefill_chunked(torch, A, H, HKV, n_layer, T, chunk, split=True, seed=
     starts = list(range(0, T, chunk))
     pos = [torch.tensor([s], dtype=torch.int32, device=dev) for s in starts]
     ws = A.PrefillWorkspace(chunk, H, HKV, T) if split else None  # the engine's path: key split for short chunks
+    gam = torch.ones((2, D), dtype=torch.float32, device=dev)
+    cs = A.rope_table(T, device=dev) if step else None
 
     def run():
         for l in range(n_layer):
             for s, p in zip(starts, pos):
                 n = min(chunk, T - s)
-                A.attn_prefill(q[l, s:s + n], kc[l], vc[l], p, shape, B=n, out=out[l, s:s + n], ws=ws)
+                if step:
+                    A.prefill_step(q[l, s:s + n], kc[l], vc[l], shape, gam[0], gam[1], cs, p, ws, B=n,
+                                   out=out[l, s:s + n])
+                else:
+                    A.attn_prefill(q[l, s:s + n], kc[l], vc[l], p, shape, B=n, out=out[l, s:s + n], ws=ws)
 
     ms = graph_ms(torch, run, reps=5, warm=1) / n_layer
     flops = A.flops_causal(T, 0, H)
-    return {"chunk": chunk, "key_split": split, "kernel_ms_per_layer": ms, "kernel_tflops": flops / (ms * 1e-3) / 1e12}
+    key = "step_ms_per_layer" if step else "kernel_ms_per_layer"
+    return {"chunk": chunk, "key_split": split, key: ms, key.replace("ms_per_layer", "tflops"): flops / (ms * 1e-3) / 1e12}
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -362,6 +371,7 @@ def main():
     if extra or args.only == "prefill-chunked":
         log("prefill configs[2] in 512-token chunks ...")
         res["prefill_chunked"] = bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512)
+        res["prefill_chunked"].update(bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512, step=True))
         log(json.dumps(res["prefill_chunked"]))
         log(json.dumps(bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512, split=False)))
     if args.only == "decode-groups":  # configs[1]'s decode at the other dense Qwen3 group sizes

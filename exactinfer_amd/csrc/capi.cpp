@@ -378,9 +378,11 @@ EI_API int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, floa
     REQUIRE(ws_bytes >= need, "workspace %zu B < %zu B (ei_attn_prefill_ws_bytes)", ws_bytes, need);
     REQUIRE(need == 0 || (ws && aligned16(ws)), "workspace must be a 16-byte aligned device pointer");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    // the attention kernel norms q itself for the full-width RoPE (Qwen3); any other rope_dim
-    // takes the prologue for every head and the plain kernel
-    const bool fuse_q = rope_dim == head_dim;
+    // the attention kernel norms q itself (full-width RoPE, every Qwen3) when the key range is
+    // split over at most two shares: each share norms the q rows it stages, so with more shares
+    // the repeated norm costs more than the q traffic it saves in the prologue (measured on
+    // 512-token chunks with 4 shares); otherwise the prologue norms every head in place first
+    const bool fuse_q = rope_dim == head_dim && ksplit <= 2;
     if (int e = hip_status(ei::launch_qkv_prepare(st, qkv, B, row_stride, n_head, n_head_kv, q_gamma, k_gamma, cs,
                                                   pos_dev, rope_dim, eps, kc, vc, fuse_q ? n_head : 0),
                            "prefill step: prologue launch"))
