@@ -22,15 +22,17 @@
 // four neighbouring blocks of the head, for odd G at most two neighbouring blocks: every
 // wave of the unit shares every K/V tile, and the unit's key range ends at its last
 // block's diagonal (a wave of an earlier block masks the few tiles past its own).  Slots
-// past the last block are idle waves (zero queries, no output).  Key group g takes the tiles kt = KS*i + g of the block's causal range and
-// keeps its own (m, l, O); the groups merge through LDS at the end of the block.  With
-// KS = 2 every SIMD runs two waves whose matrix streams interleave, each covering the
-// other's LDS waits and per-tile softmax preamble.  Inside a wave's stream the next score
-// chain alternates with this tile's P.V chains, and the next tiles' DMA instructions are
-// issued between them (on this part VALU or VMEM work outside the stream idles the pipe).
-// For short chunks at long positions (ei_attn_prefill_split) the key range of every block
-// is further split over ksplit workgroups whose unnormalised shares k_prefill_combine
-// merges.
+// past the last block are idle waves (zero queries, no output).  Key group g takes the
+// tiles kt = KS*i + g of the unit's causal range and keeps its own (m, l, O); the groups
+// merge through LDS at the end of the unit.  With KS = 2 every SIMD runs two waves whose
+// matrix streams interleave: one streams while the other waits on LDS or the per-tile
+// barrier (their VALU work still adds to the matrix time: on this part a wave's fp32 MFMA
+// stream holds the SIMD's issue).  Inside a wave's stream the next score chain alternates
+// with this tile's P.V chains, and the next tiles' DMA instructions are issued between them
+// (VMEM work outside the stream idles the pipe).  When one unit pair per KV head would not
+// fill the CUs (short chunks at long positions, GQA groups under 4 heads;
+// ei_attn_prefill_split) the key range of every unit is further split over ksplit
+// workgroups whose unnormalised shares k_prefill_combine merges.
 //
 // K/V tiles (32 keys) reach LDS by LDS DMA (global_load_lds_dwordx4) straight from the
 // cache, two tiles ahead for K and one for V, per key group:
@@ -91,9 +93,9 @@ constexpr int kLdsF = kQStageF + kSlots * kQB * kKS_F > kKS * kGroupF ? kQStageF
 
 // QK-norm + RoPE of one q row in LDS (rope_dim = 128), eight lanes per row: lane k of the row
 // holds elements 8k..8k+7 and their rotate-half partners 64+8k..64+8k+7.  Same arithmetic as the
-// prologue's head-norm (the reference's k_headnorm_rope, src/cuda/model_cuda.cu:87-105): sum of
-// squares in double, inv = float(1/sqrt(ss/128 + eps)), y = (x*inv)*gamma, then
-// (y_e, y_e+64) -> (y_e c - y_e+64 s, y_e s + y_e+64 c).  The double sum runs over the eight
+// prologue's head-norm, which follows the reference CPU path (rmsnorm, src/ops.cpp:155-160; rope,
+// src/model.cpp:23-32): sum of squares in double, inv = float(1/sqrt(ss/128 + eps)),
+// y = (x*inv)*gamma, then (y_e, y_e+64) -> (y_e c - y_e+64 s, y_e s + y_e+64 c).  The double sum runs over the eight
 // lanes' partial sums (a different order of exact products than the prologue's lane pairs; the
 // float result is the same unless the double rounds across a float boundary).
 __device__ __forceinline__ void norm_rope_q8(float* row, const float (&g)[16], const float4 (&t)[4], float eps,
