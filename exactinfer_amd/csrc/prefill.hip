@@ -225,7 +225,8 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
             const int p0 = *pos_dev + r0;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const float4* tr = reinterpret_cast<const float4*>(cs + (size_t)(p0 + min(8 * h + j, jm)) * (kHeadDim / 2) + 8 * k);
+                const float2* row = cs + (size_t)(p0 + min(8 * h + j, jm)) * (kHeadDim / 2);
+                const float4* tr = reinterpret_cast<const float4*>(row + 8 * k);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) t[h][i] = tr[i];
             }
