@@ -345,6 +345,8 @@ def main():
               "(one process per GPU would shard decode by KV head and prefill by head); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
+    from exactinfer_amd import build as B
+    B.ensure_built()  # builds only when nothing is built
     from exactinfer_amd import attention as A
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")

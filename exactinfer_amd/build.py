@@ -51,5 +51,11 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+def ensure_built() -> Path:
+    """Build the library only when it is absent (the entry scripts' convenience: tests, smoke and
+    the bench load what is built; the library loader itself never builds and fails loudly)."""
+    return LIB if LIB.exists() else build()
+
+
 if __name__ == "__main__":
     print(build(verbose=True))

@@ -10,6 +10,8 @@ if str(ROOT) not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built libei_attn.so")
+    from exactinfer_amd import build as B
+    B.ensure_built()  # builds only when nothing is built
 
 
 @pytest.fixture(scope="session")
