@@ -10,7 +10,10 @@
 // it is within 1e-5 of float64 attention and no farther from it than the reference is
 // (the rule of tests/parity.py).
 //
-// Usage: engine_test <n_layer> <n_head> <n_head_kv> <prompt> <max_batch> <decode_steps> <n_ctx>
+// Usage: engine_test <n_layer> <n_head> <n_head_kv> <prompt> <max_batch> <decode_steps> <n_ctx> [graph]
+// With "graph", decode steps after the first replay one captured hipGraph of all layers' attention
+// sub-steps, the way the reference replays its decode step (src/cuda/model_cuda.cu:1848-1859): the
+// device position advances between replays, the graph itself never changes.
 // Prints one JSON line; exit status 0 when every check passes.
 #include <hip/hip_runtime.h>
 
@@ -19,6 +22,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <stdexcept>
+#include <string>
 #include <vector>
 
 #include "../../exactinfer_amd/host/hip_attention.h"
@@ -44,10 +48,11 @@ static double rel_err_row(const float* got, const float* ref, int n) {
 }
 
 int main(int argc, char** argv) {
-    if (argc != 8) {
-        std::fprintf(stderr, "usage: engine_test n_layer n_head n_head_kv prompt max_batch decode_steps n_ctx\n");
+    if (argc != 8 && !(argc == 9 && std::string(argv[8]) == "graph")) {
+        std::fprintf(stderr, "usage: engine_test n_layer n_head n_head_kv prompt max_batch decode_steps n_ctx [graph]\n");
         return 2;
     }
+    const bool use_graph = argc == 9;
     ei::AttnConfig cfg;
     cfg.n_layer = std::atoi(argv[1]);
     cfg.n_head = std::atoi(argv[2]);
@@ -104,21 +109,15 @@ int main(int argc, char** argv) {
         hc(hipMemcpy(d_qg, qg.data(), qg.size() * 4, hipMemcpyHostToDevice));
         hc(hipMemcpy(d_kg, kg.data(), kg.size() * 4, hipMemcpyHostToDevice));
         std::vector<float> hq(size_t(max_batch) * QKV), ha(size_t(max_batch) * H * D);
-        auto run_chunk = [&](int pos0, int B) {
-            eng.begin_chunk(pos0, B);
-            for (int l = 0; l < L; ++l) {
-                for (int b = 0; b < B; ++b)
-                    std::copy(raw_row(l, pos0 + b), raw_row(l, pos0 + b) + QKV, hq.begin() + size_t(b) * QKV);
-                hc(hipMemcpyAsync(d_qkv, hq.data(), size_t(B) * QKV * 4, hipMemcpyHostToDevice, st));
-                eng.layer(l, d_qkv, QKV, d_qg + size_t(l) * D, d_kg + size_t(l) * D, d_att);
-                hc(hipMemcpyAsync(ha.data(), d_att, size_t(B) * H * D * 4, hipMemcpyDeviceToHost, st));
-                hc(hipStreamSynchronize(st));
+        // compare B attention rows of layer l (host copy `ha`, rows pos0..pos0+B-1) with the reference
+        auto check_rows = [&](int l, int pos0, int B, const float* ha_rows) {
+            {
                 for (int b = 0; b < B; ++b) {
                     const int t = pos0 + b;
                     double row_worst = 0;
                     for (int h = 0; h < H; ++h) {
                         const float* ref = ratt.data() + ((size_t(l) * total + t) * H + h) * D;
-                        row_worst = std::max(row_worst, rel_err_row(ha.data() + (size_t(b) * H + h) * D, ref, D));
+                        row_worst = std::max(row_worst, rel_err_row(ha_rows + (size_t(b) * H + h) * D, ref, D));
                     }
                     if (row_worst > 1e-5) {  // long-context fallback against float64
                         std::vector<double> ex(size_t(H) * D);
@@ -129,7 +128,7 @@ int main(int argc, char** argv) {
                         double got_x = 0, ref_x = 0;
                         for (int h = 0; h < H; ++h) {
                             const float* x = exf.data() + size_t(h) * D;
-                            got_x = std::max(got_x, rel_err_row(ha.data() + (size_t(b) * H + h) * D, x, D));
+                            got_x = std::max(got_x, rel_err_row(ha_rows + (size_t(b) * H + h) * D, x, D));
                             ref_x = std::max(ref_x,
                                              rel_err_row(ratt.data() + ((size_t(l) * total + t) * H + h) * D, x, D));
                         }
@@ -140,8 +139,51 @@ int main(int argc, char** argv) {
                 }
             }
         };
+        auto run_chunk = [&](int pos0, int B) {
+            eng.begin_chunk(pos0, B);
+            for (int l = 0; l < L; ++l) {
+                for (int b = 0; b < B; ++b)
+                    std::copy(raw_row(l, pos0 + b), raw_row(l, pos0 + b) + QKV, hq.begin() + size_t(b) * QKV);
+                hc(hipMemcpyAsync(d_qkv, hq.data(), size_t(B) * QKV * 4, hipMemcpyHostToDevice, st));
+                eng.layer(l, d_qkv, QKV, d_qg + size_t(l) * D, d_kg + size_t(l) * D, d_att);
+                hc(hipMemcpyAsync(ha.data(), d_att, size_t(B) * H * D * 4, hipMemcpyDeviceToHost, st));
+                hc(hipStreamSynchronize(st));
+                check_rows(l, pos0, B, ha.data());
+            }
+        };
         for (int p = 0; p < prompt; p += max_batch) run_chunk(p, std::min(max_batch, prompt - p));
-        for (int t = prompt; t < total; ++t) run_chunk(t, 1);
+        if (!use_graph) {
+            for (int t = prompt; t < total; ++t) run_chunk(t, 1);
+        } else if (steps > 0) {
+            run_chunk(prompt, 1);  // first step eagerly: launch set-up happens outside the capture
+            float *g_qkv, *g_att;
+            hc(hipMalloc(&g_qkv, size_t(L) * QKV * 4));
+            hc(hipMalloc(&g_att, size_t(L) * H * D * 4));
+            hipGraph_t graph = nullptr;
+            hipGraphExec_t exec = nullptr;
+            std::vector<float> gq(size_t(L) * QKV), ga(size_t(L) * H * D);
+            for (int t = prompt + 1; t < total; ++t) {
+                eng.begin_chunk(t, 1);  // uploads the position; the captured graph reads it on the device
+                for (int l = 0; l < L; ++l) std::copy(raw_row(l, t), raw_row(l, t) + QKV, gq.begin() + size_t(l) * QKV);
+                hc(hipMemcpyAsync(g_qkv, gq.data(), gq.size() * 4, hipMemcpyHostToDevice, st));
+                if (!exec) {
+                    hc(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+                    for (int l = 0; l < L; ++l)
+                        eng.layer(l, g_qkv + size_t(l) * QKV, QKV, d_qg + size_t(l) * D, d_kg + size_t(l) * D,
+                                  g_att + size_t(l) * H * D);
+                    hc(hipStreamEndCapture(st, &graph));
+                    hc(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+                }
+                hc(hipGraphLaunch(exec, st));
+                hc(hipMemcpyAsync(ga.data(), g_att, ga.size() * 4, hipMemcpyDeviceToHost, st));
+                hc(hipStreamSynchronize(st));
+                for (int l = 0; l < L; ++l) check_rows(l, t, 1, ga.data() + size_t(l) * H * D);
+            }
+            if (exec) hc(hipGraphExecDestroy(exec));
+            if (graph) hc(hipGraphDestroy(graph));
+            hc(hipFree(g_qkv));
+            hc(hipFree(g_att));
+        }
 
         std::vector<float> hk(size_t(n_ctx) * KD), hv(size_t(n_ctx) * KD);
         for (int l = 0; l < L; ++l) {
@@ -170,8 +212,8 @@ int main(int argc, char** argv) {
     const bool ok = worst <= 1e-5 && caches_exact && threw_ok;
     std::printf("{\"ok\": %s, \"max_rel_err\": %.3e, \"f64_fallback_rows\": %d, \"caches_bit_exact\": %s, "
                 "\"out_of_range_thrown\": %s, \"layers\": %d, \"prompt\": %d, \"max_batch\": %d, "
-                "\"decode_steps\": %d}\n",
+                "\"decode_steps\": %d, \"graph\": %s}\n",
                 ok ? "true" : "false", worst, fallback_rows, caches_exact ? "true" : "false",
-                threw_ok ? "true" : "false", L, prompt, max_batch, steps);
+                threw_ok ? "true" : "false", L, prompt, max_batch, steps, use_graph ? "true" : "false");
     return ok ? 0 : 1;
 }

@@ -43,3 +43,13 @@ def test_long_prompt_in_512_chunks_then_decode():
     prefill splits each query block's key range over workgroups; then decode steps at ctx ~4000."""
     rc, res = _run(1, 32, 8, 4000, 512, 8, 4100)
     assert rc == 0 and res["ok"], res
+
+
+def test_decode_steps_replay_one_captured_graph():
+    """The reference replays its decode step as one CUDA graph (src/cuda/model_cuda.cu:1848-1859);
+    here every decode step after the first replays one captured hipGraph of all layers'
+    HipAttention::layer calls, with only the device-resident position changing (two layers, 4B
+    heads, 200-token prompt, 40 steps)."""
+    rc, res = _run(2, 32, 8, 200, 128, 40, 300, "graph")
+    assert rc == 0 and res["ok"] and res["graph"], res
+    assert res["caches_bit_exact"]
