@@ -158,11 +158,12 @@ def test_decode_long_context_split_combine(orc, gpu):
     assert ok16, msg16
 
 
-@pytest.mark.parametrize("nseq,empty", [(12, ()), (12, (3, 7)), (40, (0, 39))])
-def test_decode_batched_ragged(orc, gpu, nseq, empty):
+@pytest.mark.parametrize("nseq,empty,H", [(12, (), 16), (12, (3, 7), 16), (40, (0, 39), 16), (12, (5,), 40)])
+def test_decode_batched_ragged(orc, gpu, nseq, empty, H):
     """Ragged offsets and lengths; nseq 12 plans a key split per sequence, nseq 40 (320 (seq, KV
-    head) units) one workgroup each.  Sequences of length 0 (`empty`) must come out as zeros."""
-    H, HKV = 16, 8
+    head) units) one workgroup each; H = 40 runs groups of 5 on the 8-head kernel.  Sequences of
+    length 0 (`empty`) must come out as zeros."""
+    HKV = 8
     rng = np.random.default_rng(5 + nseq)
     lens = rng.integers(1, 3000, nseq).astype(np.int32)
     lens[1], lens[2] = 1, 64
@@ -472,7 +473,7 @@ def _gather(pool, table, s, n, bs):
 
 @pytest.mark.parametrize("bs", [16, 64])
 def test_decode_paged_matches_reference(orc, gpu, bs):
-    H, HKV = 16, 8
+    H, HKV = (16, 8) if bs == 16 else (40, 8)  # bs 64: groups of 5 on the 8-head kernel
     rng = np.random.default_rng(40 + bs)
     lens = np.array([700, 300, 1, 0, 129, 2048, 64], np.int32)
     shared = 3  # sequences 0 and 1 share their first 3 blocks (a cached common prefix)
