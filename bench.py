@@ -39,19 +39,20 @@ def log(msg: str) -> None:
 
 
 def parse():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--prefill-steps", type=int, default=5)
+    ap = argparse.ArgumentParser(description="One JSON line: configs[1] decode (headline) + configs[2] prefill.")
+    ap.add_argument("--gpus", type=int, default=1, help="GPUs (this build measures one)")
+    ap.add_argument("--steps", type=int, default=256, help="timed decode steps (one token through 36 layers each)")
+    ap.add_argument("--warmup", type=int, default=20, help="untimed decode steps before the timed ones")
+    ap.add_argument("--prefill-steps", type=int, default=5, help="timed 36-layer prefill steps of 2048 tokens")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch the per-layer kernels eagerly")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the parity-case shapes reported beside the headline (configs[3], configs[4] contiguous "
                          "and paged, configs[2] in 512-token chunks)")
-    ap.add_argument("--only", choices=["decode", "decode-groups", "prefill", "prefill-chunked", "prefill-groups", "longctx",
-                                         "batched", "batched-paged"],
-                    default=None)
+    ap.add_argument("--only", choices=["decode", "decode-groups", "prefill", "prefill-chunked", "prefill-groups",
+                                       "longctx", "batched", "batched-paged"], default=None,
+                    help="run one workload and print its result (decode: the headline line without the extras; "
+                         "decode-groups / prefill-groups: the dense Qwen3 GQA group sizes)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
     return ap.parse_args()
