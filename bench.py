@@ -51,7 +51,7 @@ def parse():
                          "and paged, configs[2] in 512-token chunks)")
     ap.add_argument("--only", choices=["decode", "decode-groups", "prefill", "prefill-chunked", "prefill-groups",
                                        "longctx", "batched", "batched-paged"], default=None,
-                    help="run one workload and print its result (decode: the headline line without the extras; "
+                    help="run one workload and print its result (decode: the headline line without prefill and extras; "
                          "decode-groups / prefill-groups: the dense Qwen3 GQA group sizes)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
