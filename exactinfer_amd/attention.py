@@ -116,6 +116,13 @@ class DecodeWorkspace:
         self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
         _capi.call("ei_attn_workspace_init", _stream(), self.buf.data_ptr(), self.nbytes)
 
+    def status(self) -> int:
+        """The workspace's sticky status word (uint32 at nbytes - 256; bit 0: the splits of one
+        (sequence, KV head) ran on different XCDs, against the placement the in-kernel split
+        merge relies on).  Synchronises the stream."""
+        word = self.buf[self.nbytes - 256:self.nbytes - 252].cpu()
+        return int(word.view(torch.int32)[0]) & 0xFFFFFFFF
+
 
 def attn_decode(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos_dev: torch.Tensor, shape: AttnShape,
                 ws: DecodeWorkspace, scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:

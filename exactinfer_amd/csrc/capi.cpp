@@ -60,13 +60,21 @@ int check_rope(int rope_dim, int head_dim) {
     return EI_OK;
 }
 
+// the fused decode steps copy the RoPE row (rope_dim/2 float pairs) in whole 16-byte pieces
+int check_rope_fused_decode(int rope_dim, int head_dim) {
+    if (int e = check_rope(rope_dim, head_dim)) return e;
+    if (rope_dim % 4 != 0)
+        return fail(EI_ERR_UNSUPPORTED, "rope_dim %d: the fused decode step needs a multiple of 4", rope_dim);
+    return EI_OK;
+}
+
 }  // namespace
 
 #define EI_API extern "C" __attribute__((visibility("default")))
 
 EI_API const char* ei_last_error(void) { return g_err.c_str(); }
 
-EI_API int ei_abi_version(void) { return 1; }
+EI_API int ei_abi_version(void) { return 2; }
 
 EI_API int ei_rope_table_fill(float* cs_host, int n_ctx, int rope_dim, double theta) {
     REQUIRE(cs_host != nullptr, "cs_host is null");
@@ -145,14 +153,16 @@ int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void
     const size_t need = ei::decode_ws_bytes(n_seq, a.H, a.HKV, max_kv);
     REQUIRE(ws_bytes >= need, "workspace of %zu bytes < %zu needed (ei_attn_decode_ws_bytes)", ws_bytes, need);
     const ei::DecodePlan p = ei::decode_plan(n_seq, a.HKV, max_kv, a.block_table != nullptr);
-    const size_t slots = (size_t)n_seq * a.HKV * p.nsplit;
-    const int G = ei::decode_group_slots(a.H / a.HKV);  // partials are laid out with the kernel's head slots
-    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const ei::DecodeWsLayout lay = ei::decode_ws_layout(n_seq, a.H, a.HKV, max_kv);
     char* base = static_cast<char*>(ws);
-    a.part_acc = reinterpret_cast<float*>(base);
-    a.part_ml = reinterpret_cast<float*>(base + al(slots * G * 128 * 4));
+    a.part_acc = reinterpret_cast<float*>(base);  // partials are laid out with the kernel's head slots
+    a.rec = reinterpret_cast<uint32_t*>(base + lay.rec);
+    a.status = reinterpret_cast<uint32_t*>(base + lay.status);
     a.chunk = p.chunk;
     a.nsplit = p.nsplit;
+    a.units = n_seq * a.HKV;
+    a.n_xcc = ei::device_xccs();
+    a.merge_in_kernel = ei::decode_merge_in_kernel(p.chunk);
     return hip_status(ei::launch_decode(st, a, n_seq, fused), "decode launch");
 }
 
@@ -205,7 +215,7 @@ EI_API int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride,
                           int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma, const float* cs,
                           int rope_dim, float eps, float scale, int max_kv, void* ws, size_t ws_bytes) {
     if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
-    if (int e = check_rope(rope_dim, head_dim)) return e;
+    if (int e = check_rope_fused_decode(rope_dim, head_dim)) return e;
     REQUIRE(qkv && out && kc && vc && q_gamma && k_gamma && cs, "null pointer argument");
     REQUIRE(n_seq > 0 && n_seq <= 65535, "n_seq %d out of range [1, 65535]", n_seq);
     REQUIRE(kv_len != nullptr || (pos_dev != nullptr && n_seq == 1),
@@ -286,7 +296,7 @@ EI_API int ei_decode_step_paged(ei_stream_t stream, const float* qkv, long row_s
                                 const float* cs, int rope_dim, float eps, float scale, int max_kv, void* ws,
                                 size_t ws_bytes) {
     if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
-    if (int e = check_rope(rope_dim, head_dim)) return e;
+    if (int e = check_rope_fused_decode(rope_dim, head_dim)) return e;
     REQUIRE(qkv && out && kc && vc && q_gamma && k_gamma && cs, "null pointer argument");
     REQUIRE(n_seq > 0 && n_seq <= 65535, "n_seq %d out of range [1, 65535]", n_seq);
     REQUIRE(row_stride >= (long)(n_head + 2 * n_head_kv) * head_dim, "row_stride %ld < (H+2*HKV)*head_dim",

@@ -1,14 +1,14 @@
 // decode.hip — split-K decode attention for gfx950 (one query token per sequence).
 //
-// Work decomposition: grid (nsplit, HKV, n_seq); 4 waves (long chunks, each wave a two-tile
-// ring) or 8 waves (chunks of <= 128 keys, one tile per wave).  A workgroup owns one KV head
-// of one sequence and one chunk of keys, and serves all G = H/HKV query heads of that GQA
-// group from the same K/V bytes (the reference re-reads K/V once per query head,
-// src/cuda/model_cuda.cu:1051, :1066).  Inside the chunk, wave w owns the 16-key tiles
-// w, w+NW, w+2NW, ... and runs its own online softmax over them; the waves merge once at
-// the end.  There is no workgroup barrier in the key loop.  The split plan gives every
-// (sequence, KV head) its own workgroup first and cuts keys only as far as it takes to
-// reach about one workgroup per CU.
+// Work decomposition: a 1-D grid of (sequence, KV head, key split) workgroups; 4 waves (long
+// chunks, each wave a two-tile ring) or 8 waves (chunks of <= 128 keys, one tile per wave).
+// A workgroup owns one KV head of one sequence and one chunk of keys, and serves all
+// G = H/HKV query heads of that GQA group from the same K/V bytes (the reference re-reads K/V
+// once per query head, src/cuda/model_cuda.cu:1051, :1066).  Inside the chunk, wave w owns the
+// 16-key tiles w, w+NW, w+2NW, ... and runs its own online softmax over them; the waves merge
+// once at the end.  There is no workgroup barrier between the DMA issue and the key loop.
+// The split plan gives every (sequence, KV head) its own workgroup first and cuts keys only
+// as far as it takes to reach about one workgroup per CU.
 //
 // Data movement: each wave streams its tiles HBM -> LDS with global_load_lds_dwordx4
 // (gfx950 LDS DMA: 64 lanes x 16 B = one 1 KB instruction, no VGPRs spent on landing
@@ -34,13 +34,13 @@
 // Groups of 3, 5, 6 or 7 heads run on the kernel built for the next power of two, with the
 // extra head slots idle (zero queries, never written out).
 //
-// Split combine: each workgroup writes its unnormalised partial (m, l, acc[G][128]); a
-// second, small launch (k_combine, one workgroup per query head) merges them,
-// o = sum_s e^(m_s-M) acc_s / sum_s e^(m_s-M) l_s, skipping empty splits
-// (src/cuda/model_cuda.cu:1097-1111 semantics).  The kernel boundary is what makes the
-// partials of every XCD visible; an in-kernel "last workgroup merges" scheme needs
-// device-coherent stores, loads and an atomic, and measured slower here.  A chunk
-// covering all keys (nsplit = 1) writes o directly and skips the second launch.
+// Split combine: each workgroup writes its unnormalised partial (acc[G][128], and (m, l) in a
+// one-line split record), merged as o = sum_s e^(m_s-M) acc_s / sum_s e^(m_s-M) l_s over the
+// non-empty splits (src/cuda/model_cuda.cu:1097-1111 semantics).  Long chunks merge inside
+// the launch: a unit's splits share one XCD and meet in its L2, and the workgroup that finds
+// every split record published merges (merge_splits).  Short chunks merge in a second small
+// launch (k_combine, one workgroup per query head).  A chunk covering all keys (nsplit = 1)
+// writes o directly.
 //
 // Fused variant: the workgroup also applies QK-norm + RoPE to its G query heads, and the
 // workgroup whose chunk holds the new position writes the normed K row and the V row to
@@ -49,13 +49,16 @@
 #include "common.h"
 #include "launch.h"
 
+#include <atomic>
 #include <cstdlib>
+#include <string>
 
 namespace ei {
 
 constexpr int kTile = 16;                          // keys per wave tile
 constexpr int kTileFloats = 2 * kTile * kHeadDim;  // K rows then V rows
 constexpr int kRingTiles = 8;                      // LDS ring: 8 tiles (128 KB) per workgroup
+constexpr int kRec = 32;                           // uint32s per split record: one 128-byte line
 
 // Transposing butterfly over the 8 lanes c = lane%8 (masks 1, 2, 4).  At each step a
 // lane keeps one half of its array and receives the partner's copy of that half, so N
@@ -126,26 +129,142 @@ __device__ __forceinline__ int tile_off(int row, int chunk) {
 // row holding key t0; the tile's keys are consecutive rows from there (a paged block holds
 // whole 16-key tiles).  Rows past t_end are clamped to the last visible row (valid memory; their
 // scores are masked out).
-__device__ __forceinline__ void issue_tile(const float* slot, const float* kbase, const float* vbase, size_t KD,
-                                           int t0, int t_end, int lane, size_t p0) {
+// One half of a tile: the 16 K rows (which = 0) or the 16 V rows (which = 1), 8 instructions.
+__device__ __forceinline__ void issue_half(const float* slot, const float* src, size_t KD, int t0, int t_end, int lane,
+                                           size_t p0, int which) {
     const int half = lane >> 5, s = lane & 31;
-    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(slot));
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(slot)) + which * kTile * kHeadDim * 4;
 #pragma unroll
     for (int t = 0; t < kTile / 2; ++t) {
         const int row = 2 * t + half;
         const int key = min(t0 + row, t_end - 1);
         const int chunk = s ^ ((row & 1) << 3);
-        dma16_nt(kbase + (p0 + (size_t)(key - t0)) * KD + 4 * chunk, base + t * 1024);
-    }
-#pragma unroll
-    for (int t = 0; t < kTile / 2; ++t) {
-        const int row = 2 * t + half;
-        const int key = min(t0 + row, t_end - 1);
-        const int chunk = s ^ ((row & 1) << 3);
-        dma16_nt(vbase + (p0 + (size_t)(key - t0)) * KD + 4 * chunk, base + kTile * kHeadDim * 4 + t * 1024);
+        dma16_nt(src + (p0 + (size_t)(key - t0)) * KD + 4 * chunk, base + t * 1024);
     }
 }
 
+__device__ __forceinline__ void issue_tile(const float* slot, const float* kbase, const float* vbase, size_t KD,
+                                           int t0, int t_end, int lane, size_t p0) {
+    issue_half(slot, kbase, KD, t0, t_end, lane, p0, 0);
+    issue_half(slot, vbase, KD, t0, t_end, lane, p0, 1);
+}
+
+
+// In-kernel split merge.  Loads miss the CU's L1 and read the XCD's L2 (buffer loads with
+// sc0); the resource is based at one unit's partials, so 32-bit offsets always suffice.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBufferDword3 = 0x00020000;  // raw 32-bit data, gfx9-family buffer resource word 3
+
+__device__ __forceinline__ float4 ld_l2_f4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 1);
+    return make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z), __uint_as_float(x.w));
+}
+__device__ __forceinline__ float2 ld_l2_f2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 1);
+    return make_float2(__uint_as_float(x.x), __uint_as_float(x.y));
+}
+
+__device__ __forceinline__ void fma4(float w, const float4 v, float4& acc) {
+    acc.x = fmaf(w, v.x, acc.x);
+    acc.y = fmaf(w, v.y, acc.y);
+    acc.z = fmaf(w, v.z, acc.z);
+    acc.w = fmaf(w, v.w, acc.w);
+}
+
+// Merge the S split partials of one unit (G head slots, the first Gr real) into out[Gr][128]:
+// o = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s over the non-empty splits (m in log2
+// units), the split-softmax combine of src/cuda/model_cuda.cu:1097-1111.
+// Thread t owns float4 column t % (32 G) of splits t / (32 G), t / (32 G) + SG, ...; the
+// first batch of its accumulator loads is in flight while each wave turns the (m, l) of its
+// heads into weights (LDS); the SG column partials are summed in a fixed order, so the result
+// does not depend on which workgroup merges.  `lds` is free LDS of >= G*256 + 64 +
+// NT*4 floats.
+template <int G, int NT>
+__device__ __forceinline__ void merge_splits(const DecodeArgs& a, size_t head_slot, int S, int Gr, float* out,
+                                             int tid, float* lds) {
+    constexpr int D = kHeadDim, NCOLS = G * 32, SG = NT / NCOLS, NB = 8;
+    static_assert(SG >= 1, "one thread per float4 column at least");
+    const int col = tid % NCOLS, sg = tid / NCOLS, g = col >> 5, d4 = col & 31;
+    const __amdgpu_buffer_rsrc_t racc = __builtin_amdgcn_make_buffer_rsrc(
+        a.part_acc + head_slot * S * G * D, 0, S * G * D * 4, kBufferDword3);
+    const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(
+        a.rec + head_slot * S * kRec, 0, S * kRec * 4, kBufferDword3);
+    float* wsh = lds;                                         // [G][256] split weights
+    float* lsh = lds + G * kDecodeMaxSplits;                  // [G] weighted l sums
+    float4* red = reinterpret_cast<float4*>(lsh + 64);        // [SG][NCOLS] column partials
+    const uint32_t col_off = (uint32_t)(g * D + 4 * d4) * 4;  // bytes within one split's partial
+    const uint32_t split_bytes = G * D * 4;
+    float4 v[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {  // out-of-range offsets read as zero (buffer bounds)
+        const int s = sg + k * SG;
+        v[k] = ld_l2_f4(racc, s < S ? (uint32_t)s * split_bytes + col_off : 0x80000000u);
+    }
+    const int lane = tid & 63;
+    for (int hg = tid >> 6; hg < Gr; hg += NT / 64) {  // weights of head hg: one wave
+        float mv[kDecodeMaxSplits / 64], lv[kDecodeMaxSplits / 64];
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kDecodeMaxSplits / 64; ++k) {
+            const int s = lane + 64 * k;
+            const float2 ml = s < S ? ld_l2_f2(rml, (uint32_t)(s * kRec + 2 + 2 * hg) * 4) : make_float2(-INFINITY, 0.f);
+            mv[k] = ml.x;
+            lv[k] = ml.y;
+            M = fmaxf(M, ml.x);
+        }
+        M = wave_max(M);
+        float L = 0.f;
+#pragma unroll
+        for (int k = 0; k < kDecodeMaxSplits / 64; ++k) {
+            const int s = lane + 64 * k;
+            const float wv = mv[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv[k] - M);  // empty split: skipped
+            if (s < S) wsh[hg * kDecodeMaxSplits + s] = wv;
+            L = fmaf(wv, lv[k], L);
+        }
+        L = wave_sum(L);
+        if (lane == 0) lsh[hg] = L;
+    }
+    __syncthreads();
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (g < Gr) {
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            const int s = sg + k * SG;
+            if (s < S) fma4(wsh[g * kDecodeMaxSplits + s], v[k], acc);
+        }
+        for (int s0 = sg + NB * SG; s0 < S; s0 += NB * SG) {
+#pragma unroll
+            for (int k = 0; k < NB; ++k) {
+                const int s = s0 + k * SG;
+                v[k] = ld_l2_f4(racc, s < S ? (uint32_t)s * split_bytes + col_off : 0x80000000u);
+            }
+#pragma unroll
+            for (int k = 0; k < NB; ++k) {
+                const int s = s0 + k * SG;
+                if (s < S) fma4(wsh[g * kDecodeMaxSplits + s], v[k], acc);
+            }
+        }
+    }
+    if (SG > 1) {
+        red[sg * NCOLS + col] = acc;
+        __syncthreads();
+    }
+    if (sg == 0 && g < Gr) {
+#pragma unroll
+        for (int j = 1; j < SG; ++j) {
+            const float4 t = red[j * NCOLS + col];
+            acc.x += t.x;
+            acc.y += t.y;
+            acc.z += t.z;
+            acc.w += t.w;
+        }
+        const float L = lsh[g];
+        const float4 o = L > 0.f ? make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);  // kv_len 0: zeros
+        *reinterpret_cast<float4*>(out + (size_t)g * D + 4 * d4) = o;
+    }
+}
 
 // NW waves per workgroup, each with a ring of kRingTiles/NW tile slots: 4 waves x 2 slots
 // streams long chunks with one tile always in flight behind the one being scored; 8 waves
@@ -166,9 +285,35 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     __shared__ __align__(16) float knew[4][D];             // fused: [0] K row (raw, then normed), [1] V row, [2] scratch
     __shared__ __align__(16) float stage[4 * D];           // fused: [0] q gamma, [1] k gamma, [2..3] RoPE row
 
-    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    // Grid placement.  Workgroup b runs on XCD b % n_xcc.  With the in-kernel merge, every split
+    // of one (sequence, KV head) unit sits on the same XCD, so the partials meet in its L2;
+    // otherwise workgroup b takes split b % S of unit b / S, so an XCD streams the same key rows
+    // of neighbouring KV heads (4 KB cache rows read by one XCD close together in time: ~2%
+    // faster than a unit per XCD for short chunks).
+    const int S = a.nsplit;
+    int split, kvh, seq, unit;
+    {
+        const uint32_t b = blockIdx.x;
+        if (a.merge_in_kernel) {
+            const uint32_t nx = (uint32_t)a.n_xcc, x = b % nx, i = b / nx, lu = i / (uint32_t)S;
+            split = (int)(i - lu * (uint32_t)S);
+            unit = (int)(lu * nx + x);
+        } else {
+            unit = (int)(b / (uint32_t)S);
+            split = (int)(b - (uint32_t)unit * S);
+        }
+        if (unit >= a.units) return;  // padding slot of the last XCD round
+        seq = unit / a.HKV;
+        kvh = unit - seq * a.HKV;
+    }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane >> 3, c = lane & 7;
+    // in-kernel merge: this split's flag and this launch's epoch (read now, used at the end)
+    // (the record line is also brought into the L2 here, long before it is written and read)
+    uint32_t* unit_rec = a.rec + (size_t)unit * S * kRec;
+    uint32_t* my_rec = unit_rec + split * kRec;
+    uint32_t epoch = 0;
+    if (S > 1 && tid == 0) epoch = *my_rec + 1u;
     const int len = a.kv_len ? a.kv_len[seq] : (*a.pos_dev + 1);
     const size_t KD = (size_t)a.HKV * D;
     const size_t row0 = a.kv_offset ? (size_t)a.kv_offset[seq] : 0;
@@ -181,7 +326,9 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     float* kbase = a.kc + row0 * KD + (size_t)kvh * D;
     float* vbase = a.vc + row0 * KD + (size_t)kvh * D;
     const int t_begin = split * a.chunk;
-    const int t_end = min(len, t_begin + a.chunk);
+    // the last split takes every key past the plan (a kv_len above the planned max_kv is
+    // still attended in full, and the fused step still finds the new row's owner)
+    const int t_end = split == S - 1 ? len : min(len, t_begin + a.chunk);
     const int pos = len > 0 ? len - 1 : 0;  // a zero-length sequence has no new row; keep the table index valid
     const float* qrow = a.q + (size_t)seq * a.q_stride;
     const int Gr = a.H / a.HKV;  // heads of this KV head (<= G; heads Gr..G-1 are padding)
@@ -210,10 +357,19 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     auto tile_row = [&](int t0) -> size_t {
         if (!btab) return (size_t)t0;
         const int i = (t0 - tw0) / kStride;
+        if (i >= 128) return phys(t0);  // only a last split extended past the plan gets here
         return (size_t)(uint32_t)(i < 64 ? __builtin_amdgcn_readlane(lane_row, i)
                                          : __builtin_amdgcn_readlane(lane_row2, i - 64));
     };
     const bool owner = FUSED && t_begin <= pos && pos < t_end;
+    const size_t pos_row = owner ? phys(pos) : 0;  // read before any DMA is in flight
+    // The waves' DMA issue is back-pressured by the CU's request queue, so a wave spends most
+    // of the stream waiting to get its instructions accepted.  Nothing waits at a workgroup
+    // barrier behind that issue: wave 0 loads and norms q and publishes it (`q_ready`), and
+    // each wave starts on its tiles as soon as q is ready and its own rows have landed.
+    __shared__ int q_ready;
+    if (tid == 0) q_ready = 0;
+    __syncthreads();
     if (w == 0) {
         const uint32_t qa = __builtin_amdgcn_readfirstlane(lds_addr(qs));
 #pragma unroll
@@ -221,15 +377,17 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
             if (1024 * i < Gr * D * 4) dma_block(qrow + (size_t)h0 * D + 256 * i, qa + 1024 * i, Gr * D * 4 - 1024 * i, lane);
         if constexpr (FUSED) {
             dma_block(a.q_gamma, __builtin_amdgcn_readfirstlane(lds_addr(stage)), D * 4, lane);
+            // the RoPE row: rope_dim*4 bytes, a multiple of 16 (the entry points require rope_dim % 4 == 0)
             dma_block(reinterpret_cast<const float*>(a.cs + (size_t)pos * (a.rope_dim >> 1)),
                       __builtin_amdgcn_readfirstlane(lds_addr(stage + 2 * D)), a.rope_dim * 4, lane);
+            if (owner) {
+                dma_block(qrow + (size_t)a.H * D + (size_t)kvh * D, __builtin_amdgcn_readfirstlane(lds_addr(knew[0])),
+                          D * 4, lane);
+                dma_block(qrow + (size_t)(a.H + a.HKV) * D + (size_t)kvh * D,
+                          __builtin_amdgcn_readfirstlane(lds_addr(knew[1])), D * 4, lane);
+                dma_block(a.k_gamma, __builtin_amdgcn_readfirstlane(lds_addr(stage + D)), D * 4, lane);
+            }
         }
-    } else if (w == 1 && owner) {
-        dma_block(qrow + (size_t)a.H * D + (size_t)kvh * D, __builtin_amdgcn_readfirstlane(lds_addr(knew[0])), D * 4,
-                  lane);
-        dma_block(qrow + (size_t)(a.H + a.HKV) * D + (size_t)kvh * D,
-                  __builtin_amdgcn_readfirstlane(lds_addr(knew[1])), D * 4, lane);
-        dma_block(a.k_gamma, __builtin_amdgcn_readfirstlane(lds_addr(stage + D)), D * 4, lane);
     }
     int ntiles0 = 0;
 #pragma unroll
@@ -239,34 +397,38 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
                        tile_row(tw0 + i * kStride));
             ++ntiles0;
         }
-    if (w <= 1) {  // this wave's prologue DMA (older than its tiles) has landed
+    if (w == 0) {
+        // the prologue DMA (older than this wave's tiles) has landed
         if (kRing == 2 && ntiles0 == 2) wait_vmcnt<2 * kTile>();
         else if (ntiles0 >= 1) wait_vmcnt<kTile>();
         else wait_vmcnt<0>();
-    }
-    if (G > Gr)  // padding heads: zero queries (finite scores, never written out)
-        for (int i = Gr * D + tid; i < G * D; i += kThreads) qs[i] = 0.f;
-    __syncthreads();
-
-    if constexpr (FUSED) {
-        const float2* cs_row = reinterpret_cast<const float2*>(stage + 2 * D);
-        for (int g = w; g < Gr; g += kWaves) {  // in place: raw q -> normed, roped q
-            float o0, o1;
-            norm_rope_head(qs + g * D, stage, cs_row, a.rope_dim, a.eps, qs + g * D, lane, &o0, &o1);
-            qs[g * D + lane] = o0;
-            qs[g * D + lane + 64] = o1;
+        if (G > Gr)  // padding heads: zero queries (finite scores, never written out)
+            for (int i = Gr * D + lane; i < G * D; i += 64) qs[i] = 0.f;
+        if constexpr (FUSED) {
+            const float2* cs_row = reinterpret_cast<const float2*>(stage + 2 * D);
+            for (int g = 0; g < Gr; ++g) {  // in place: raw q -> normed, roped q
+                float o0, o1;
+                norm_rope_head(qs + g * D, stage, cs_row, a.rope_dim, a.eps, knew[2], lane, &o0, &o1);
+                qs[g * D + lane] = o0;
+                qs[g * D + lane + 64] = o1;
+            }
+            if (owner) {
+                float o0, o1;
+                norm_rope_head(knew[0], stage + D, cs_row, a.rope_dim, a.eps, knew[2], lane, &o0, &o1);
+                knew[0][lane] = o0;
+                knew[0][lane + 64] = o1;
+                __builtin_amdgcn_wave_barrier();
+                // the new K row (lanes 0-31) and V row (lanes 32-63) to the cache, one float4 each
+                float* dst = (lane < 32 ? kbase : vbase) + pos_row * KD + 4 * (lane & 31);
+                *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(&knew[lane >> 5][4 * (lane & 31)]);
+            }
         }
-        if (owner && w == kWaves - 1) {
-            float o0, o1;
-            norm_rope_head(knew[0], stage + D, cs_row, a.rope_dim, a.eps, knew[2], lane, &o0, &o1);
-            knew[0][lane] = o0;
-            knew[0][lane + 64] = o1;
-        }
-        __syncthreads();
-        if (owner && tid < 2 * D) {
-            float* dst = (tid < D ? kbase : vbase) + phys(pos) * KD + (tid & (D - 1));
-            *dst = knew[tid >> 7][tid & (D - 1)];
-        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): q (and the new K row) are in LDS
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) __hip_atomic_store(&q_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+        while (__hip_atomic_load(&q_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+            __builtin_amdgcn_s_sleep(1);
     }
 
     // q operand of the score phase: held in registers for up to 4 heads; 8 heads would take 128
@@ -404,28 +566,25 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
 
     // thread t < NCOL merges float4 column (g, d4)
     const size_t head_slot = (size_t)seq * a.HKV + kvh;
-    const size_t slot = head_slot * a.nsplit + split;
-    const int S = a.nsplit;
+    const size_t slot = head_slot * S + split;
     const int gcol = (tid % NCOL) / 32, d4 = (tid % NCOL) % 32;
     float Mw = -INFINITY, Lw = 0.f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid < NCOL) {
-        float mws[kWaves];
+    if (tid < NCOL) {  // every wave wrote its (m, l, acc); a wave without keys has m = -inf, l = 0, acc = 0
+        float mws[kWaves], lws[kWaves];
+        float4 v[kWaves];
 #pragma unroll
         for (int ww = 0; ww < kWaves; ++ww) {
-            mws[ww] = t_begin + kTile * ww < t_end ? wml[ww][gcol] : -INFINITY;  // waves without keys: nothing
+            mws[ww] = wml[ww][gcol];
+            lws[ww] = wml[ww][G + gcol];
+            v[ww] = *reinterpret_cast<const float4*>(&ring[ww * (kRing * kTileFloats) + gcol * D + 4 * d4]);
             Mw = fmaxf(Mw, mws[ww]);
         }
 #pragma unroll
         for (int ww = 0; ww < kWaves; ++ww) {
-            if (mws[ww] == -INFINITY) continue;
-            const float wv = __builtin_amdgcn_exp2f(mws[ww] - Mw);
-            Lw = fmaf(wv, wml[ww][G + gcol], Lw);
-            const float4 v = *reinterpret_cast<const float4*>(&ring[ww * (kRing * kTileFloats) + gcol * D + 4 * d4]);
-            o.x = fmaf(wv, v.x, o.x);
-            o.y = fmaf(wv, v.y, o.y);
-            o.z = fmaf(wv, v.z, o.z);
-            o.w = fmaf(wv, v.w, o.w);
+            const float wv = mws[ww] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mws[ww] - Mw);
+            Lw = fmaf(wv, lws[ww], Lw);
+            fma4(wv, v[ww], o);
         }
     }
 
@@ -442,12 +601,56 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
         return;
     }
 
-    // unnormalised partial of this split; k_combine merges the splits in a second launch
-    // (the kernel boundary makes these plain stores visible to every XCD)
-    if (tid < NCOL && gcol < Gr) {
-        *reinterpret_cast<float4*>(a.part_acc + (slot * G + gcol) * D + 4 * d4) = o;
-        if (d4 == 0) *reinterpret_cast<float2*>(a.part_ml + (slot * G + gcol) * 2) = make_float2(Mw, Lw);
+    // unnormalised partial of this split: acc rows, then the split's record line (epoch, and
+    // (m, l) of each head slot), written whole by one instruction so the line is valid in the L2
+    if (tid < NCOL && gcol < Gr) *reinterpret_cast<float4*>(a.part_acc + (slot * G + gcol) * D + 4 * d4) = o;
+    __shared__ float mlsh[2 * G];
+    __shared__ int is_last;
+    if (tid < NCOL && d4 == 0) {
+        mlsh[2 * gcol] = Mw;
+        mlsh[2 * gcol + 1] = Lw;
     }
+    const bool merging = a.merge_in_kernel;
+    if (merging) wait_vmcnt<0>();  // this thread's acc stores are in the L2 before the record is
+    __syncthreads();
+    if (w == 0) {
+        const uint32_t e = __builtin_amdgcn_readfirstlane(epoch);
+        uint32_t xcc = 0;  // the XCD this workgroup runs on (record word 1)
+        if (merging) asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        if (lane < kRec)
+            my_rec[lane] = lane == 0 ? e : lane == 1 ? xcc : lane >= 2 && lane < 2 + 2 * G ? __float_as_uint(mlsh[lane - 2]) : 0u;
+        if (merging) {
+            // In-kernel merge.  Every split of the unit ran on this XCD, so the partials meet in
+            // its L2: a store is acknowledged by the L2 (vmcnt), and loads that miss the CU's L1
+            // read it there.  Each workgroup publishes its record with this launch's epoch (the
+            // record's previous value + 1) and reads the epochs of all the unit's records; one
+            // that finds every record at its epoch merges.  The workgroup whose record reached
+            // the L2 last always finds them all, since the others' were acknowledged before it;
+            // if several find them all, each writes the same bits.  No atomics (they serialise
+            // on one address) and no L2 write-back or invalidate (a device-wide fence costs more
+            // than the whole decode on this part).
+            wait_vmcnt<0>();  // the record is in the L2 before the others are read
+            bool all = true, same_xcd = true;
+            for (int s0 = 0; s0 < S; s0 += 64) {
+                const int sx = s0 + lane;
+                uint32_t f = e, fx = xcc;
+                if (sx < S) {
+                    f = __hip_atomic_load(unit_rec + sx * kRec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    fx = __hip_atomic_load(unit_rec + sx * kRec + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+                all = all && __builtin_amdgcn_ballot_w64(f != e) == 0;
+                same_xcd = same_xcd && __builtin_amdgcn_ballot_w64(fx != xcc) == 0;
+            }
+            // the placement the protocol relies on (workgroups b and b + n_xcc share an XCD; the
+            // dispatcher's starting XCD may rotate between launches) held for every split
+            if (lane == 0 && all && !same_xcd) atomicOr(a.status, 1u);
+            if (lane == 0) is_last = all;
+        }
+    }
+    if (!merging) return;  // k_combine merges the splits in a second launch
+    __syncthreads();
+    if (!is_last) return;
+    merge_splits<G, kThreads>(a, head_slot, S, Gr, a.out + (size_t)seq * a.H * D + (size_t)h0 * D, tid, ring);
 }
 
 // Split combine as a separate launch: grid (n_seq * H), 128 threads (thread = d).  All
@@ -463,7 +666,7 @@ __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
     const int kvh = hq / Gr, g = hq % Gr;
     const int S = a.nsplit, tid = threadIdx.x;
     const size_t head_slot = (size_t)seq * a.HKV + kvh;
-    const float* pml = a.part_ml + (head_slot * S * G + g) * 2;
+    const float* pml = reinterpret_cast<const float*>(a.rec + head_slot * S * kRec) + 2 + 2 * g;
     const float* pa = a.part_acc + (head_slot * S * G + g) * D + tid;
     constexpr int B = 32;
     float acc = 0.f;
@@ -479,7 +682,7 @@ __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
 #pragma unroll
                 for (int k = 0; k < kDecodeMaxSplits / 64; ++k) {
                     const int s = tid + 64 * k;
-                    const float2 ml = s < S ? *reinterpret_cast<const float2*>(pml + (size_t)s * G * 2)
+                    const float2 ml = s < S ? *reinterpret_cast<const float2*>(pml + (size_t)s * kRec)
                                             : make_float2(-INFINITY, 0.f);
                     mv[k] = ml.x;
                     lv[k] = ml.y;
@@ -543,25 +746,35 @@ DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged) {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv) {
+DecodeWsLayout decode_ws_layout(int n_seq, int H, int HKV, int max_kv) {
     // sized for the larger of the paged and contiguous plans, so one workspace serves both
     const DecodePlan p0 = decode_plan(n_seq, HKV, max_kv, false), p1 = decode_plan(n_seq, HKV, max_kv, true);
     const DecodePlan p = p0.nsplit >= p1.nsplit ? p0 : p1;
     const size_t slots = (size_t)n_seq * HKV * p.nsplit;
     const int G = decode_group_slots(H / HKV);
-    return align256(slots * G * kHeadDim * 4) + align256(slots * G * 2 * 4);
+    DecodeWsLayout l;
+    l.rec = align256(slots * G * kHeadDim * 4);
+    l.status = l.rec + align256(slots * kRec * 4);
+    l.total = l.status + 256;
+    return l;
 }
+
+size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv) { return decode_ws_layout(n_seq, H, HKV, max_kv).total; }
 
 template <int G, int NW>
 static hipError_t launch_gw(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused) {
-    const dim3 grid(a.nsplit, a.HKV, n_seq);
+    // 1-D grid in XCD rounds: slot b runs on XCD b % n_xcc; the units of XCD x are x, x + n_xcc, ...
+    // each with its nsplit workgroups (units past the end leave at once)
+    const long rounds = ((long)a.units + a.n_xcc - 1) / a.n_xcc;
+    const dim3 grid((unsigned)(rounds * a.n_xcc * a.nsplit));
     const size_t lds = (size_t)kRingTiles * kTileFloats * sizeof(float);  // 128 KB
     static std::atomic<bool> opted[2];
     const void* f = fused ? (const void*)k_decode<G, true, NW> : (const void*)k_decode<G, false, NW>;
     if (const hipError_t e = opt_in_lds(opted[fused], f, lds); e != hipSuccess) return e;
     if (fused) k_decode<G, true, NW><<<grid, 64 * NW, lds, st>>>(a);
     else k_decode<G, false, NW><<<grid, 64 * NW, lds, st>>>(a);
-    if (a.nsplit > 1) k_combine<G><<<n_seq * a.H, 128, 0, st>>>(a);
+    if (a.nsplit > 1 && !a.merge_in_kernel)
+        k_combine<G><<<(unsigned)(n_seq * a.H), 128, 0, st>>>(a);
     return hipGetLastError();
 }
 
@@ -572,6 +785,34 @@ static hipError_t launch_g(hipStream_t st, const DecodeArgs& a, int n_seq, bool 
 }
 
 int decode_group_slots(int g) { return g <= 1 ? 1 : g <= 2 ? 2 : g <= 4 ? 4 : g <= 8 ? 8 : 0; }
+
+int device_xccs() {
+    // XCDs of the current device (8 on an MI355X in SPX mode), queried once per device
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || v < 1 || v > 16) v = 1;
+    cache[dev].store(v, std::memory_order_relaxed);
+    return v;
+}
+
+bool decode_merge_in_kernel(int chunk) {
+    // Chunks of more than 128 keys (the 4-wave streaming kernel) merge in-kernel: configs[3]'s
+    // 1024-key chunks run ~4.5% faster than with the second launch.  Short chunks (one tile per
+    // wave, e.g. ctx 4096 over 32 splits) keep the second launch: there the partial stores are
+    // acknowledged only once the memory queues drain after the stream (0.6-2 us, against
+    // 0.18 us on an idle part), which costs more than the launch.  EI_DECODE_MERGE=launch or
+    // =kernel forces either.
+    static const int forced = [] {
+        const char* e = std::getenv("EI_DECODE_MERGE");
+        if (!e) return -1;
+        const std::string v(e);
+        return v == "launch" ? 0 : v == "kernel" ? 1 : -1;
+    }();
+    return forced >= 0 ? forced == 1 : chunk > 8 * kTile;
+}
 
 hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused) {
     // any group of 1..8 heads runs on the next kernel built for 1, 2, 4 or 8 heads

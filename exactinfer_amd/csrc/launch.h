@@ -41,6 +41,12 @@ constexpr int kDecodeMaxSplits = 256;
 constexpr int kDecodePagedMaxChunk = 8192;  // 4 waves x 128 tiles of 16 keys
 DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged);
 size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv);
+// byte offsets of the workspace parts: partial accumulators at 0, then the split records and
+// the status word (the last 256 bytes)
+struct DecodeWsLayout {
+    size_t rec, status, total;
+};
+DecodeWsLayout decode_ws_layout(int n_seq, int H, int HKV, int max_kv);
 int decode_group_slots(int g);  // heads per KV head the decode kernel is built for (0: unsupported)
 
 struct DecodeArgs {
@@ -59,7 +65,12 @@ struct DecodeArgs {
     float scale;
     int chunk, nsplit;
     float* part_acc;        // [n_seq*HKV*nsplit][G][128]
-    float* part_ml;         // [n_seq*HKV*nsplit][G][2]
+    uint32_t* rec;          // [n_seq*HKV*nsplit][32]: split record line, word 0 the merge epoch,
+                            // words 2+2g, 3+2g the (m, l) of head slot g (float bits)
+    uint32_t* status;       // sticky word: bit 0 set when a workgroup ran on another XCD than its grid slot says
+    int units;              // n_seq * HKV
+    int n_xcc;              // XCDs the grid is spread over (workgroup b runs on XCD b % n_xcc)
+    bool merge_in_kernel;   // the last workgroup of a unit merges its splits (else k_combine does)
     // fused prologue
     const float* q_gamma;
     const float* k_gamma;
@@ -69,6 +80,8 @@ struct DecodeArgs {
 };
 
 hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused);
+int device_xccs();              // XCDs of the current device
+bool decode_merge_in_kernel(int chunk);  // split merge inside the decode launch for this chunk size
 hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes);
 
 // ------------------------------------------------------------------ prefill.hip

@@ -81,11 +81,18 @@ int ei_qkv_prepare(ei_stream_t stream, float* qkv, int rows, long row_stride, in
 
 /* ------------------------------------------------------------------ decode (split-K)
  * Workspace for the decode entry points: per (sequence, kv head, key split) partial
- * (m, l, acc).  max_kv bounds the number of visible keys of any sequence over the
- * workspace's life (it fixes the split grid, so a captured graph stays valid as positions
- * advance).  The contents are scratch: no initialisation is required
- * (ei_attn_workspace_init zero-fills it, with a kernel rather than a memset, and is
- * optional).  Calls that share a workspace must not overlap in time. */
+ * (m, l, acc), one arrival counter per (sequence, kv head) for the in-kernel split merge,
+ * and a status word in its last 256 bytes.  max_kv sizes the split grid (fixed, so a
+ * captured graph stays valid as positions advance); a sequence longer than max_kv is still
+ * attended in full (its last split takes the excess keys), only more slowly.
+ * The workspace must be zero-filled once before its first use, by ei_attn_workspace_init
+ * (a fill kernel, not a memset, so it may be captured) or any other zero fill; every decode
+ * call leaves the counters at zero again.  Status word (uint32 at ws + ws_bytes - 256, as
+ * sized by ei_attn_decode_ws_bytes): bit 0 is set, and stays set, if the splits of one
+ * (sequence, kv head) were ever found on different XCDs, against the round-robin placement
+ * the in-kernel merge relies on (never seen on MI355X; that merge is then unreliable: set
+ * EI_DECODE_MERGE=launch for the two-launch combine).  Calls that share a workspace must not
+ * overlap in time. */
 size_t ei_attn_decode_ws_bytes(int n_seq, int n_head, int n_head_kv, int max_kv);
 int ei_attn_workspace_init(ei_stream_t stream, void* ws, size_t ws_bytes);
 
@@ -108,7 +115,7 @@ int ei_attn_decode_batched(ei_stream_t stream, const float* q, long q_stride, fl
                            int n_head_kv, int head_dim, float scale, int max_kv, void* ws, size_t ws_bytes);
 
 /* Fused decode step: ei_qkv_prepare + ei_attn_decode for one token per sequence in one
- * decode launch (plus the small split-combine launch when the keys are split).  qkv row s (at qkv + s*row_stride, [Q|K|V] raw projections) is read only;
+ * decode launch (the split combine happens inside it; rope_dim must be a multiple of 4).  qkv row s (at qkv + s*row_stride, [Q|K|V] raw projections) is read only;
  * the normed+roped K row and the V row are written to cache row kv_offset[s] + pos_s,
  * pos_s = kv_len[s]-1 (or *pos_dev when kv_len is NULL; then n_seq must be 1 and
  * kv_offset may be NULL).  out [n_seq][n_head][128].  Equivalent to the per-layer

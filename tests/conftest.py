@@ -28,3 +28,20 @@ def gpu():
         pytest.skip("no GPU")
     from exactinfer_amd import attention as A
     return A
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Which branch of the attention gate each recorded case passed by (tests/parity.py)."""
+    from tests.parity import ATTN_RTOL, EVIDENCE
+    if not EVIDENCE:
+        return
+    tr = terminalreporter
+    tr.section(f"attention parity evidence (bar {ATTN_RTOL:g})")
+    worst = max(e[2] for e in EVIDENCE)
+    fb = [e for e in EVIDENCE if e[1] != "reference"]
+    tr.write_line(f"{len(EVIDENCE)} cases; worst rel err vs reference {worst:.3e}; "
+                  f"{len(fb)} passed by the float64 fallback or failed")
+    for case, branch, e_ref, e_gx, e_rx, plain in EVIDENCE:
+        if branch != "reference" or e_ref > 0.5 * ATTN_RTOL:
+            extra = "" if e_gx is None else f"; vs float64 {e_gx:.3e} (reference vs float64 {e_rx:.3e})"
+            tr.write_line(f"  {branch:16s} {case}: vs reference {e_ref:.3e}{extra}; plain |d|/|ref| {plain:.3e}")

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     L = _capi.lib()
     for name in _declared():
         assert isinstance(getattr(L, name), ctypes._CFuncPtr), name
-    assert L.ei_abi_version() == 1
+    assert L.ei_abi_version() == 2
 
 
 def test_rope_table_fill_host_matches_oracle(orc):
@@ -124,3 +124,14 @@ def test_paged_argument_errors():
         _capi.call("ei_attn_decode_paged", None, p, 4096, p, p, p, p, 4, 16, p, 2, 32, 8, 128, 0.1, 128, p, 1 << 20)
     with pytest.raises(_capi.EiError, match="block_table and kv_len"):
         _capi.call("ei_attn_decode_paged", None, p, 4096, p, p, p, None, 8, 16, p, 2, 32, 8, 128, 0.1, 128, p, 1 << 20)
+
+
+def test_fused_decode_rope_dim_multiple_of_4():
+    from exactinfer_amd import _capi
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    with pytest.raises(_capi.EiError, match="rope_dim 126"):
+        _capi.call("ei_decode_step", None, p, 6144, p, p, p, None, None, p, 1, 32, 8, 128, p, p, p, 126, 1e-6, 0.1,
+                   4096, p, 1 << 30)
+    with pytest.raises(_capi.EiError, match="rope_dim 62"):
+        _capi.call("ei_decode_step_paged", None, p, 6144, p, p, p, p, 8, 16, p, 1, 32, 8, 128, p, p, p, 62, 1e-6,
+                   0.1, 128, p, 1 << 30)
