@@ -147,7 +147,8 @@ EI_API int ei_attn_workspace_init(ei_stream_t stream, void* ws, size_t ws_bytes)
 
 namespace {
 
-int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void* ws, size_t ws_bytes, bool fused) {
+int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void* ws, size_t ws_bytes, bool fused,
+                  bool launch_combine = false) {
     REQUIRE(max_kv > 0, "max_kv %d must be positive", max_kv);
     REQUIRE(ws != nullptr && aligned16(ws), "workspace missing or not 16-byte aligned");
     const size_t need = ei::decode_ws_bytes(n_seq, a.H, a.HKV, max_kv);
@@ -162,7 +163,7 @@ int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void
     a.nsplit = p.nsplit;
     a.units = n_seq * a.HKV;
     a.n_xcc = ei::device_xccs();
-    a.merge_in_kernel = ei::decode_merge_in_kernel(p.chunk);
+    a.merge_in_kernel = !launch_combine && ei::decode_merge_in_kernel(p.chunk);
     return hip_status(ei::launch_decode(st, a, n_seq, fused), "decode launch");
 }
 
@@ -210,10 +211,12 @@ EI_API int ei_attn_decode_batched(ei_stream_t stream, const float* q, long q_str
     return decode_common(static_cast<hipStream_t>(stream), a, n_seq, max_kv, ws, ws_bytes, false);
 }
 
-EI_API int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc, float* vc,
-                          const int64_t* kv_offset, const int* kv_len, const int* pos_dev, int n_seq, int n_head,
-                          int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma, const float* cs,
-                          int rope_dim, float eps, float scale, int max_kv, void* ws, size_t ws_bytes) {
+namespace {
+
+int decode_step_impl(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc, float* vc,
+                     const int64_t* kv_offset, const int* kv_len, const int* pos_dev, int n_seq, int n_head,
+                     int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma, const float* cs,
+                     int rope_dim, float eps, float scale, int max_kv, void* ws, size_t ws_bytes, bool no_alloc) {
     if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
     if (int e = check_rope_fused_decode(rope_dim, head_dim)) return e;
     REQUIRE(qkv && out && kc && vc && q_gamma && k_gamma && cs, "null pointer argument");
@@ -242,7 +245,39 @@ EI_API int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride,
     a.cs = reinterpret_cast<const float2*>(cs);
     a.rope_dim = rope_dim;
     a.eps = eps;
-    return decode_common(static_cast<hipStream_t>(stream), a, n_seq, max_kv, ws, ws_bytes, true);
+    if (no_alloc) {
+        REQUIRE(max_kv > 0, "max_kv %d must be positive", max_kv);
+        const size_t need = ei::decode_ws_bytes(n_seq, n_head, n_head_kv, max_kv);
+        REQUIRE(need <= ei::kDecodeScratchBytes,
+                "n_seq %d, n_head %d, n_head_kv %d, max_kv %d need %zu bytes of scratch; the allocation-free step has "
+                "%zu (use ei_decode_step with a workspace)",
+                n_seq, n_head, n_head_kv, max_kv, need, ei::kDecodeScratchBytes);
+        if (int e = hip_status(ei::decode_scratch(&ws), "scratch address lookup")) return e;
+        ws_bytes = ei::kDecodeScratchBytes;
+    }
+    // the allocation-free step always merges the splits in the second launch: its partials are
+    // fully rewritten by every call, so nothing in the shared scratch has to start at zero
+    return decode_common(static_cast<hipStream_t>(stream), a, n_seq, max_kv, ws, ws_bytes, true, no_alloc);
+}
+
+}  // namespace
+
+EI_API int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc, float* vc,
+                          const int64_t* kv_offset, const int* kv_len, const int* pos_dev, int n_seq, int n_head,
+                          int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma, const float* cs,
+                          int rope_dim, float eps, float scale, int max_kv, void* ws, size_t ws_bytes) {
+    return decode_step_impl(stream, qkv, row_stride, out, kc, vc, kv_offset, kv_len, pos_dev, n_seq, n_head,
+                            n_head_kv, head_dim, q_gamma, k_gamma, cs, rope_dim, eps, scale, max_kv, ws, ws_bytes,
+                            false);
+}
+
+EI_API int ei_decode_step_noalloc(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc,
+                                  float* vc, const int64_t* kv_offset, const int* kv_len, const int* pos_dev, int n_seq,
+                                  int n_head, int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma,
+                                  const float* cs, int rope_dim, float eps, float scale, int max_kv) {
+    return decode_step_impl(stream, qkv, row_stride, out, kc, vc, kv_offset, kv_len, pos_dev, n_seq, n_head,
+                            n_head_kv, head_dim, q_gamma, k_gamma, cs, rope_dim, eps, scale, max_kv, nullptr, 0,
+                            true);
 }
 
 namespace {

@@ -825,6 +825,29 @@ hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fu
     }
 }
 
+// ------------------------------------------------------------------ allocation-free scratch
+// Device-resident scratch for ei_decode_step_noalloc: each GPU the library runs on holds its
+// own copy until the process ends.  Host code never passes `scratch` itself (its host-side name
+// is not a device address): decode_scratch() looks up this device's address once, with the
+// device current, and callers use that pointer.
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+hipError_t decode_scratch(void** ptr) {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<void*> addr[kMaxDevices];
+    int dev = 0;
+    if (const hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    void* p = addr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {  // first call on this device (concurrent first calls look up the same address)
+        if (const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        addr[dev].store(p, std::memory_order_release);
+    }
+    *ptr = p;
+    return hipSuccess;
+}
+
 hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes) {
     const size_t n = bytes / 4;
     if (n == 0) return hipSuccess;

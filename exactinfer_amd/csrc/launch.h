@@ -83,6 +83,9 @@ hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fu
 int device_xccs();              // XCDs of the current device
 bool decode_merge_in_kernel(int chunk);  // split merge inside the decode launch for this chunk size
 hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes);
+// allocation-free decode: this device's address of a static scratch array of kDecodeScratchBytes
+constexpr size_t kDecodeScratchBytes = size_t(4) << 20;
+hipError_t decode_scratch(void** ptr);
 
 // ------------------------------------------------------------------ prefill.hip
 // Key split across workgroups for short chunks: ksplit shares per query block, merged by a

@@ -126,6 +126,22 @@ int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride, float*
                    int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma, const float* cs,
                    int rope_dim, float eps, float scale, int max_kv, void* ws, size_t ws_bytes);
 
+/* Allocation-free fused decode step.  No counterpart in the reference: it is for callers that
+ * cannot allocate or pass a workspace (code under HIP graph capture set up before any
+ * workspace exists, tight serving loops, harnesses that forbid allocation).  Same arguments,
+ * semantics and results as ei_decode_step without (ws, ws_bytes); the split partials live in a
+ * static device array of 4 MiB per GPU, held until the process ends, so the call allocates
+ * nothing.  A shape whose ei_attn_decode_ws_bytes(n_seq, n_head, n_head_kv, max_kv) exceeds
+ * 4 MiB is rejected with EI_ERR_ARG (one sequence at H32/HKV8 takes 0.53 MiB up to max_kv
+ * 32768; 64 sequences at H16/HKV8 take 0.56 MiB at max_kv 8192 and 4.5 MiB, too much, at
+ * 65536; 256 sequences at H32/HKV8 and max_kv 4096 take 4.25 MiB, too much).  Every call on one GPU shares that array:
+ * calls that overlap in time on one GPU (two streams, two threads) race and must not be made.
+ * The splits are always merged by the second small launch. */
+int ei_decode_step_noalloc(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc, float* vc,
+                           const int64_t* kv_offset, const int* kv_len, const int* pos_dev, int n_seq, int n_head,
+                           int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma, const float* cs,
+                           int rope_dim, float eps, float scale, int max_kv);
+
 /* ------------------------------------------------------------------ paged KV (multi-sequence serving)
  * Sequence s's key t lives in cache row block_table[s*max_blocks + t/block_size]*block_size
  * + t%block_size of the shared pool kc/vc (rows of n_head_kv*128 floats); block_size is a

@@ -1,0 +1,74 @@
+"""The allocation-free fused decode step (ei_decode_step_noalloc) against ei_decode_step with a
+workspace: two calls in a row through the C ABI, the second with a smaller input, each equal
+bit for bit to the workspace entry point on the same state (both merge their splits with the
+second launch for these shapes), cache appends included."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from tests.parity import bits_equal
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def _noalloc(gpu, qkv, kc, vc, shape, qg, kg, cs, max_kv, out, pos_dev=None, kv_offset=None, kv_len=None):
+    from exactinfer_amd import _capi
+    n_seq = qkv.shape[0]
+    p = lambda t: None if t is None else t.data_ptr()
+    _capi.call("ei_decode_step_noalloc", gpu._stream(), qkv.data_ptr(), qkv.stride(0), out.data_ptr(), kc.data_ptr(),
+               vc.data_ptr(), p(kv_offset), p(kv_len), p(pos_dev), n_seq, shape.n_head, shape.n_head_kv,
+               shape.head_dim, qg.data_ptr(), kg.data_ptr(), cs.data_ptr(), shape.rope_dim, float(shape.eps),
+               float(gpu.default_scale()), max_kv)
+
+
+def test_noalloc_decode_step_matches_workspace_step(orc, gpu):
+    import torch
+    # call 1: configs[1]'s layer (H32/HKV8, ctx 4096, one sequence); call 2: a smaller ragged batch
+    cases = [dict(H=32, HKV=8, lens=[4096], max_kv=4096, seed=7000),
+             dict(H=16, HKV=8, lens=[300, 1, 77], max_kv=512, seed=7100)]
+    for c in cases:
+        H, HKV, lens = c["H"], c["HKV"], np.array(c["lens"], np.int32)
+        shape = gpu.AttnShape(H, HKV)
+        n_seq = len(lens)
+        offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+        rows = int(lens.sum())
+        k, v = orc.normal((rows, HKV * D), c["seed"]), orc.normal((rows, HKV * D), c["seed"] + 1)
+        qkv = _dev(orc.normal((n_seq, shape.qkv), c["seed"] + 2))
+        qg, kg = _dev(orc.gamma(D, c["seed"] + 3)), _dev(orc.gamma(D, c["seed"] + 4))
+        cs = gpu.rope_table(c["max_kv"])
+        kc_a, vc_a, kc_b, vc_b = _dev(k), _dev(v), _dev(k), _dev(v)
+        out_a = torch.full((n_seq, H, D), float("nan"), device="cuda")
+        if n_seq == 1:
+            pos = torch.tensor([int(lens[0]) - 1], dtype=torch.int32, device="cuda")
+            _noalloc(gpu, qkv, kc_a, vc_a, shape, qg, kg, cs, c["max_kv"], out_a, pos_dev=pos)
+            ws = gpu.DecodeWorkspace(1, H, HKV, c["max_kv"])
+            out_b = gpu.decode_step(qkv, kc_b, vc_b, shape, qg, kg, cs, ws, pos_dev=pos)
+        else:
+            od, ld = _dev(offs), _dev(lens)
+            _noalloc(gpu, qkv, kc_a, vc_a, shape, qg, kg, cs, c["max_kv"], out_a, kv_offset=od, kv_len=ld)
+            ws = gpu.DecodeWorkspace(n_seq, H, HKV, c["max_kv"])
+            out_b = gpu.decode_step(qkv, kc_b, vc_b, shape, qg, kg, cs, ws, kv_offset=od, kv_len=ld)
+        assert bits_equal(_host(out_a), _host(out_b)), f"output differs for {c}"
+        assert bits_equal(_host(kc_a), _host(kc_b)) and bits_equal(_host(vc_a), _host(vc_b)), f"cache differs for {c}"
+
+
+def test_noalloc_rejects_shapes_beyond_its_scratch(gpu):
+    from exactinfer_amd import _capi
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    with pytest.raises(_capi.EiError, match="allocation-free"):
+        _capi.call("ei_decode_step_noalloc", None, p, 6144, p, p, p, p, p, None, 256, 32, 8, 128, p, p, p, 128, 1e-6,
+                   0.1, 4096)
