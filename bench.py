@@ -25,13 +25,21 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by
-# the factor a plain 256 MiB copy needs (FETCH x2.000, WRITE x1.000); profiles/*_hbm_traffic.md
-# and profiles/prefill_configs2_kernel_trace.md hold the runs.
-TRAFFIC_DECODE_PER_LAYER = (16539 + 303.5) * 2.0 * 1024 + (528 + 16) * 1024  # k_decode + k_combine
-TRAFFIC_PREFILL = 24704 * 2.0 * 1024 + 32773 * 1024                          # k_prefill
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 D = 128
+PROFILES = ROOT / "profiles"
+
+
+def profile_traffic(name: str):
+    """HBM bytes per launch recorded in a committed rocprofv3 summary (profiles/<name>): the line
+    `traffic_bytes_per_launch: N` holds FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by
+    the factor a plain copy of known size needs.  None when the summary or the line is absent."""
+    import re
+    f = PROFILES / name
+    if not f.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", f.read_text())
+    return float(m.group(1)) if m else None
 
 
 def log(msg: str) -> None:
@@ -50,7 +58,8 @@ def parse():
                     help="skip the parity-case shapes reported beside the headline (configs[3], configs[4] contiguous "
                          "and paged, configs[2] in 512-token chunks)")
     ap.add_argument("--only", choices=["decode", "decode-groups", "prefill", "prefill-chunked", "prefill-groups",
-                                       "longctx", "batched", "batched-paged"], default=None,
+                                       "longctx", "batched", "batched-paged", "stream-ceiling", "configs0"],
+                    default=None,
                     help="run one workload and print its result (decode: the headline line without prefill and extras; "
                          "decode-groups / prefill-groups: the dense Qwen3 GQA group sizes)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
@@ -160,6 +169,29 @@ def bench_decode(torch, A, H, HKV, n_layer, ctx, steps, warmup, use_graph, spike
     }
 
 
+def bench_stream_ceiling(torch, A, H, HKV, n_layer, ctx, reps=50, seed=1000):
+    """The decode plan's memory traffic alone (ei_stream_ceiling): n_layer launches over separate
+    caches of ctx positions in one graph, the same grid and DMA pattern as the decode."""
+    from exactinfer_amd import _capi
+    dev = "cuda"
+    kd = HKV * D
+    kc = torch.empty((n_layer, ctx, kd), dtype=torch.float32, device=dev)
+    vc = torch.empty_like(kc)
+    for l in range(n_layer):
+        A.synth_fill(kc[l], seed + 2 * l)
+        A.synth_fill(vc[l], seed + 2 * l + 1)
+    sink = torch.empty((HKV * 256,), dtype=torch.float32, device=dev)
+
+    def run():
+        for l in range(n_layer):
+            _capi.call("ei_stream_ceiling", A._stream(), kc[l].data_ptr(), vc[l].data_ptr(), HKV, ctx, sink.data_ptr())
+
+    ms = graph_ms(torch, run, reps=reps, warm=5) / n_layer
+    kv_bytes = 2.0 * ctx * kd * 4
+    return {"kernel_ms": ms, "kv_bytes_per_launch": kv_bytes, "gbs": kv_bytes / (ms * 1e-3) / 1e9,
+            "decode_bytes_per_launch": A.decode_bytes(ctx, H, HKV)}
+
+
 def bench_batched(torch, A, steps, warmup, use_graph, seed=3000, block_size=0):
     """1.7B shape, 64 sequences with kv_len ~ U[256, 8192], 28 layers.  block_size > 0: the same
     sequences in a paged pool (shuffled blocks of block_size rows, fused paged step)."""
@@ -264,20 +296,26 @@ def bench_prefill(torch, A, H, HKV, n_layer, T, steps, warmup, seed=2000):
     t = Timer(torch)
     tot = 0.0
     for _ in range(steps):
-        qkv.copy_(qkv_src)  # the prologue normalises in place: restore raw projections (untimed)
+        qkv.copy_(qkv_src)  # the prologue normalises the K heads in place: restore raw projections (untimed)
         t.start()
         step()
         tot += t.stop_ms()
     ms = tot / steps
     flops_layer = A.flops_causal(T, 0, H)
-    # the dominant kernel alone: n_layer attention launches in one graph, on q rows normed by
-    # the full prologue (the same contraction the fused step runs; it also norms q as it stages it)
+    # the step's two kernels per layer (key prologue + k_prefill<true>) replayed as one graph of
+    # n_layer steps; replays re-norm the already normed K heads in place, which keeps them bounded
+    # and runs the same arithmetic
+    qkv.copy_(qkv_src)
+    step_layer_ms = graph_ms(torch, step, reps=max(steps, 3), warm=1) / n_layer
+    # the attention kernel without the q norm (k_prefill<false>), on q rows the full prologue normed
     qkv.copy_(qkv_src)
     for l in range(n_layer):
         A.qkv_prepare(qkv[l], shape, gam[l, 0], gam[l, 1], cs, pos_dev, kc[l], vc[l])
-    kern_ms = graph_ms(torch, lambda: [attn(l) for l in range(n_layer)], reps=5, warm=1) / n_layer
-    return {"ms_per_step": ms, "tflops": flops_layer * n_layer / (ms * 1e-3) / 1e12, "kernel_ms": kern_ms,
-            "kernel_tflops": flops_layer / (kern_ms * 1e-3) / 1e12, "flops_per_launch": flops_layer}
+    plain_ms = graph_ms(torch, lambda: [attn(l) for l in range(n_layer)], reps=5, warm=1) / n_layer
+    return {"ms_per_step": ms, "tflops": flops_layer * n_layer / (ms * 1e-3) / 1e12,
+            "step_layer_ms": step_layer_ms, "step_layer_tflops": flops_layer / (step_layer_ms * 1e-3) / 1e12,
+            "plain_kernel_ms": plain_ms, "plain_kernel_tflops": flops_layer / (plain_ms * 1e-3) / 1e12,
+            "flops_per_launch": flops_layer}
 
 
 def bench_prefill_chunked(torch, A, H, HKV, n_layer, T, chunk, split=True, seed=2100, step=False):
@@ -315,13 +353,31 @@ def bench_prefill_chunked(torch, A, H, HKV, n_layer, T, chunk, split=True, seed=
 
 
 # ---------------------------------------------------------------- CPU baseline
-def cpu_baseline(budget_s: float = 12.0):
-    """Reference CPU attention loop (oracle restatement of src/model.cpp:191-214, OpenMP over
-    heads) on configs[1]'s shape: decode layers with ctx 4096 until the time budget is spent."""
+def cpu_info():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count() or 1
+
+
+def cpu_baseline(budget_s: float = 10.0):
+    """The reference CPU attention (the oracle's restatement of src/model.cpp:191-214, one token at
+    a time as src/model.cpp:138-140 runs it, OpenMP over query heads) on this host:
+    - the headline value: decode layers at configs[1]'s shape (H32/HKV8, ctx 4096) for ~budget_s;
+    - configs[0]: one 0.6B-shape layer (H16/HKV8), 512 prompt tokens then 128 decode steps;
+    - configs[2]'s prefill (H32/HKV8, 2048 tokens), timed on every 16th row and scaled by FLOPs."""
     import numpy as np
+    from exactinfer_amd import attention as A
     from oracle import oracle as O
     cores = min(int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1), 64)
     O.set_threads(cores)
+    model, nproc = cpu_info()
+    # configs[1] decode
     H, HKV, T = 32, 8, 4096
     k = O.normal((T, HKV, D), 1)
     v = O.normal((T, HKV, D), 2)
@@ -332,11 +388,87 @@ def cpu_baseline(budget_s: float = 12.0):
         O.attn_decode(q, k, v, T, H, HKV, D)
         n += 1
     dt = (time.perf_counter() - t0) / n
-    gbs = (4.0 * (2 * T * HKV * D + 2 * H * D)) / dt / 1e9
+    gbs = A.decode_bytes(T, H, HKV) / dt / 1e9
+    # prompt of 512 tokens then 128 decode steps, one token at a time
+    H0, HKV0, P, G0 = 16, 8, 512, 128
+    k0 = O.normal((P + G0, HKV0, D), 11)
+    v0 = O.normal((P + G0, HKV0, D), 12)
+    q0 = O.normal((P + G0, H0, D), 13)
+    t0 = time.perf_counter()
+    for t in range(P):
+        O.attn_decode(q0[t], k0, v0, t + 1, H0, HKV0, D)
+    t_pre = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for t in range(P, P + G0):
+        O.attn_decode(q0[t], k0, v0, t + 1, H0, HKV0, D)
+    t_dec = time.perf_counter() - t0
+    dec_bytes0 = sum(A.decode_bytes(t + 1, H0, HKV0) for t in range(P, P + G0))
+    # configs[2] prefill on a row sample, scaled by the FLOPs of the rows timed
+    H2, HKV2, T2, stride = 32, 8, 2048, 16
+    k2 = O.normal((T2, HKV2, D), 21)
+    v2 = O.normal((T2, HKV2, D), 22)
+    q2 = O.normal((T2 // stride, H2, D), 23)
+    rows = list(range(stride - 1, T2, stride))
+    t0 = time.perf_counter()
+    for i, b in enumerate(rows):
+        O.attn_decode(q2[i], k2, v2, b + 1, H2, HKV2, D)
+    t_rows = time.perf_counter() - t0
+    flops_rows = sum(4.0 * D * (b + 1) * H2 for b in rows)
+    pre_tflops = flops_rows / t_rows / 1e12
     _ = np
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "cpu_model": model, "nproc": nproc,
             "sample": f"{n} single-layer decode steps at configs[1] shape (H32/HKV8, ctx 4096), "
-                      f"{dt * 1e3:.2f} ms per layer, {dt * 36 * 1e3:.1f} ms per 36-layer token"}
+                      f"{dt * 1e3:.2f} ms per layer, {dt * 36 * 1e3:.1f} ms per 36-layer token",
+            "configs0": {"workload": "Qwen3-0.6B shape H16/HKV8, one layer: 512 prompt tokens then 128 decode steps, "
+                                     "one token at a time (src/model.cpp:138-140)",
+                         "prefill_ms": round(t_pre * 1e3, 2), "prefill_tok_s": round(P / t_pre, 1),
+                         "prefill_tflops": round(A.flops_causal(P, 0, H0) / t_pre / 1e12, 5),
+                         "decode_ms": round(t_dec * 1e3, 2), "decode_tok_s": round(G0 / t_dec, 1),
+                         "decode_gbs": round(dec_bytes0 / t_dec / 1e9, 3)},
+            "prefill_configs2": {"workload": "H32/HKV8, 2048-token causal prefill, one token at a time; every 16th "
+                                             "row timed and scaled by the FLOPs of the rows timed",
+                                 "tflops": round(pre_tflops, 5),
+                                 "ms_per_layer_scaled": round(A.flops_causal(T2, 0, H2) / (pre_tflops * 1e12) * 1e3,
+                                                              1)}}
+
+
+def bench_configs0_gpu(torch, A):
+    """configs[0] on the GPU path: one 0.6B-shape layer, the 512-token prompt as one fused prefill
+    step, then 128 fused decode steps (each appends one row), timed with HIP events."""
+    H, HKV, P, G = 16, 8, 512, 128
+    shape = A.AttnShape(H, HKV)
+    dev = "cuda"
+    n_ctx = P + G
+    qkv = A.synth_fill(torch.empty((n_ctx, shape.qkv), dtype=torch.float32, device=dev), 600)
+    kc = torch.zeros((n_ctx, HKV * D), dtype=torch.float32, device=dev)
+    vc = torch.zeros_like(kc)
+    gam = torch.ones((2, D), dtype=torch.float32, device=dev)
+    cs = A.rope_table(n_ctx)
+    pws = A.PrefillWorkspace(P, H, HKV, n_ctx)
+    dws = A.DecodeWorkspace(1, H, HKV, n_ctx)
+    pos0 = torch.zeros(1, dtype=torch.int32, device=dev)
+    poss = [torch.tensor([t], dtype=torch.int32, device=dev) for t in range(P, n_ctx)]
+    src = qkv.clone()
+
+    def run():
+        A.prefill_step(qkv[:P], kc, vc, shape, gam[0], gam[1], cs, pos0, pws, B=P)
+        for i, t in enumerate(range(P, n_ctx)):
+            A.decode_step(qkv[t:t + 1], kc, vc, shape, gam[0], gam[1], cs, dws, pos_dev=poss[i])
+
+    run()
+    torch.cuda.synchronize()
+    qkv.copy_(src)
+    tm = Timer(torch)
+    tm.start()
+    A.prefill_step(qkv[:P], kc, vc, shape, gam[0], gam[1], cs, pos0, pws, B=P)
+    pre_ms = tm.stop_ms()
+    tm.start()
+    for i, t in enumerate(range(P, n_ctx)):
+        A.decode_step(qkv[t:t + 1], kc, vc, shape, gam[0], gam[1], cs, dws, pos_dev=poss[i])
+    dec_ms = tm.stop_ms()
+    return {"prefill_ms": pre_ms, "decode_ms_128_steps": dec_ms, "decode_us_per_step": dec_ms * 1e3 / G,
+            "note": "eager launches, one layer: launch-latency bound at this size"}
 
 
 def main():
@@ -347,7 +479,7 @@ def main():
         sys.exit(2)
     import torch
     from exactinfer_amd import build as B
-    B.ensure_built()  # builds only when nothing is built
+    B.ensure_built()  # builds only when nothing is built or a source is newer than the library
     from exactinfer_amd import attention as A
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
@@ -403,6 +535,14 @@ def main():
         res["batched_paged"] = bench_batched(torch, A, 128 if args.steps >= 128 else args.steps, 3, use_graph,
                                              block_size=64)
         log(json.dumps(res["batched_paged"]))
+    if extra or args.only == "stream-ceiling":
+        log("stream ceiling of the configs[1] decode plan ...")
+        res["stream_ceiling"] = bench_stream_ceiling(torch, A, 32, 8, 36, 4096)
+        log(json.dumps(res["stream_ceiling"]))
+    if extra or args.only == "configs0":
+        log("configs[0] on the GPU path ...")
+        res["configs0"] = bench_configs0_gpu(torch, A)
+        log(json.dumps(res["configs0"]))
     if args.only not in (None, "decode"):
         print(json.dumps(res))
         return
@@ -426,9 +566,10 @@ def main():
                                "36 launches per step in one HIP graph" if dec["graph"] else "eager launches",
                    "pct_hbm_peak": round(100 * dec["gbs"] / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(dec["kernel_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_DECODE_PER_LAYER,
-                     "kernel": "k_decode<4,true,8> + k_combine<4> (one layer)", "kernel_us": round(dec["kernel_ms"] * 1e3, 3),
-                     "bytes_per_launch": dec["bytes_per_launch"]},
+                     "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": profile_traffic("decode_configs1_hbm_traffic.md"),
+                     "kernel": "k_decode<4,true,8> + k_combine<4> (one layer, graph-timed)",
+                     "kernel_us": round(dec["kernel_ms"] * 1e3, 3), "bytes_per_launch": dec["bytes_per_launch"]},
         "cpu_baseline": cpu,
     }
     if pre is not None:
@@ -436,15 +577,20 @@ def main():
                                        "ei_prefill_step: key prologue (QK-norm + RoPE + append) + k_prefill "
                                        "(fp32 MFMA; q QK-norm + RoPE in-kernel)",
                            "tflops": round(pre["tflops"], 3), "ms_per_step": round(pre["ms_per_step"], 4),
-                           "roofline": {"bound": "mfma", "achieved": round(pre["kernel_tflops"], 3),
+                           "roofline": {"bound": "mfma", "achieved": round(pre["step_layer_tflops"], 3),
                                         "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                        "frac": round(pre["kernel_tflops"] / FP32_MFMA_PEAK_TFLOPS, 4),
-                                        "traffic": TRAFFIC_PREFILL, "kernel": "k_prefill<false> (q normed beforehand)",
-                                        "kernel_us": round(pre["kernel_ms"] * 1e3, 2),
-                                        "flops_per_launch": pre["flops_per_launch"]}}
+                                        "frac": round(pre["step_layer_tflops"] / FP32_MFMA_PEAK_TFLOPS, 4),
+                                        "traffic": profile_traffic("prefill_configs2_hbm_traffic.md"),
+                                        "kernel": "k_qkv_prepare (key heads) + k_prefill<true> (one layer of the "
+                                                  "step, graph-timed)",
+                                        "kernel_us": round(pre["step_layer_ms"] * 1e3, 2),
+                                        "flops_per_launch": pre["flops_per_launch"],
+                                        "plain_kernel": {"kernel": "k_prefill<false> (q normed beforehand)",
+                                                         "kernel_us": round(pre["plain_kernel_ms"] * 1e3, 2),
+                                                         "tflops": round(pre["plain_kernel_tflops"], 3)}}}
     # the other configs (parity-test shapes), measured beside the headline for context
     ex = {}
-    for k in ("longctx", "batched", "batched_paged", "prefill_chunked"):
+    for k in ("longctx", "batched", "batched_paged", "prefill_chunked", "stream_ceiling", "configs0"):
         if k in res:
             ex[k] = {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in res[k].items()}
             if "gbs" in res[k]:

@@ -51,10 +51,24 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+def inputs() -> list[Path]:
+    """Every file the library is built from: the sources, the private headers and the ABI header."""
+    return [PKG / s for s in SOURCES] + [CSRC / h for h in HEADERS] + [ROOT / "include" / "ei_attn.h"]
+
+
+def is_stale() -> bool:
+    """True when the library is absent or older than any file it is built from."""
+    if not LIB.exists():
+        return True
+    built = LIB.stat().st_mtime
+    return any(p.stat().st_mtime > built for p in inputs())
+
+
 def ensure_built() -> Path:
-    """Build the library only when it is absent (the entry scripts' convenience: tests, smoke and
-    the bench load what is built; the library loader itself never builds and fails loudly)."""
-    return LIB if LIB.exists() else build()
+    """Build the library when it is absent or older than a source or header (the entry scripts'
+    convenience: tests, smoke and the bench load what is built; the library loader itself never
+    builds and fails loudly)."""
+    return build() if is_stale() else LIB
 
 
 if __name__ == "__main__":

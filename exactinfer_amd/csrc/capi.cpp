@@ -437,6 +437,15 @@ EI_API int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, floa
                       "prefill step: attention launch");
 }
 
+EI_API int ei_stream_ceiling(ei_stream_t stream, const float* kc, const float* vc, int n_head_kv, int kv_len,
+                             float* sink) {
+    REQUIRE(kc && vc && sink, "null pointer argument");
+    REQUIRE(n_head_kv > 0 && kv_len > 0, "n_head_kv %d / kv_len %d", n_head_kv, kv_len);
+    REQUIRE(aligned16(kc) && aligned16(vc), "pointers must be 16-byte aligned");
+    return hip_status(ei::launch_stream_ceiling(static_cast<hipStream_t>(stream), kc, vc, n_head_kv, kv_len, sink),
+                      "stream ceiling launch");
+}
+
 EI_API int ei_synth_fill(ei_stream_t stream, float* dst, size_t n, uint64_t seed, uint64_t offset, long row_len,
                          long spike_every, float spike_mult) {
     REQUIRE(dst != nullptr || n == 0, "dst is null");

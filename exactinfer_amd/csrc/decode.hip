@@ -825,6 +825,50 @@ hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fu
     }
 }
 
+// ------------------------------------------------------------------ stream ceiling
+// The decode's memory traffic with no arithmetic: the same grid, waves, LDS-DMA instructions,
+// tile order and cache policy as k_decode<G, false, NW> for one sequence of `len` keys, each
+// wave waiting for its last tile and one lane per workgroup writing a word of it to `sink`.
+// Its duration is the floor a decode launch of this plan can reach on this part.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_stream_ceiling(const float* kc, const float* vc, int HKV, int len,
+                                                            int chunk, int nsplit, float* sink) {
+    constexpr int kRing = kRingTiles / NW, kStride = kTile * NW;
+    extern __shared__ __align__(16) float ring[];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int unit = blockIdx.x / nsplit, split = blockIdx.x - unit * nsplit;
+    if (unit >= HKV) return;
+    const size_t KD = (size_t)HKV * kHeadDim;
+    const float* kbase = kc + (size_t)unit * kHeadDim;
+    const float* vbase = vc + (size_t)unit * kHeadDim;
+    const int t_begin = split * chunk, t_end = min(len, t_begin + chunk);
+    float* wring = ring + w * (kRing * kTileFloats);
+    int slot = 0;
+    for (int t0 = t_begin + kTile * w; t0 < t_end; t0 += kStride, slot = (slot + 1) % kRing) {
+        if (t0 - (t_begin + kTile * w) >= kRing * kStride) wait_vmcnt<(kRing - 1) * kTile>();  // the slot's old tile
+        issue_tile(wring + slot * kTileFloats, kbase, vbase, KD, t0, t_end, lane, (size_t)t0);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (threadIdx.x == 0) sink[blockIdx.x] = ring[w * (kRing * kTileFloats)];
+}
+
+hipError_t launch_stream_ceiling(hipStream_t st, const float* kc, const float* vc, int HKV, int len, float* sink) {
+    const DecodePlan p = decode_plan(1, HKV, len, false);
+    const size_t lds = (size_t)kRingTiles * kTileFloats * sizeof(float);
+    const dim3 grid((unsigned)(HKV * p.nsplit));
+    if (p.chunk <= 8 * kTile) {
+        static std::atomic<bool> opted;
+        if (const hipError_t e = opt_in_lds(opted, (const void*)k_stream_ceiling<8>, lds); e != hipSuccess) return e;
+        k_stream_ceiling<8><<<grid, 512, lds, st>>>(kc, vc, HKV, len, p.chunk, p.nsplit, sink);
+    } else {
+        static std::atomic<bool> opted;
+        if (const hipError_t e = opt_in_lds(opted, (const void*)k_stream_ceiling<4>, lds); e != hipSuccess) return e;
+        k_stream_ceiling<4><<<grid, 256, lds, st>>>(kc, vc, HKV, len, p.chunk, p.nsplit, sink);
+    }
+    return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ allocation-free scratch
 // Device-resident scratch for ei_decode_step_noalloc: each GPU the library runs on holds its
 // own copy until the process ends.  Host code never passes `scratch` itself (its host-side name

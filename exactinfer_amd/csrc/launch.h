@@ -83,6 +83,8 @@ hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fu
 int device_xccs();              // XCDs of the current device
 bool decode_merge_in_kernel(int chunk);  // split merge inside the decode launch for this chunk size
 hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes);
+// the decode plan's memory traffic alone, for one sequence of len keys; sink takes one float per workgroup
+hipError_t launch_stream_ceiling(hipStream_t st, const float* kc, const float* vc, int HKV, int len, float* sink);
 // allocation-free decode: this device's address of a static scratch array of kDecodeScratchBytes
 constexpr size_t kDecodeScratchBytes = size_t(4) << 20;
 hipError_t decode_scratch(void** ptr);

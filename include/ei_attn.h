@@ -200,6 +200,13 @@ int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, float* out,
                     const float* k_gamma, const float* cs, int rope_dim, float eps, float scale, int max_kv, void* ws,
                     size_t ws_bytes);
 
+/* ------------------------------------------------------------------ measurement
+ * Not part of the reference path: the memory traffic of ei_attn_decode's plan for one sequence
+ * of kv_len keys with no arithmetic (same grid, LDS-DMA instructions, tile order and cache
+ * policy; each workgroup writes one float of what it read to sink, which must hold
+ * n_head_kv * 256 floats).  Its duration is the floor of a decode launch of that plan. */
+int ei_stream_ceiling(ei_stream_t stream, const float* kc, const float* vc, int n_head_kv, int kv_len, float* sink);
+
 /* ------------------------------------------------------------------ synthetic inputs
  * Not part of the reference path: fills n floats with the counter-based N(0,1)
  * generator (element e = stream element offset+e of `seed`), multiplying by spike_mult
