@@ -58,7 +58,7 @@ def parse():
                     help="skip the parity-case shapes reported beside the headline (configs[3], configs[4] contiguous "
                          "and paged, configs[2] in 512-token chunks)")
     ap.add_argument("--only", choices=["decode", "decode-groups", "prefill", "prefill-chunked", "prefill-groups",
-                                       "longctx", "batched", "batched-paged", "stream-ceiling", "configs0"],
+                                       "longctx", "batched", "batched-paged", "stream-ceiling", "configs0", "project"],
                     default=None,
                     help="run one workload and print its result (decode: the headline line without prefill and extras; "
                          "decode-groups / prefill-groups: the dense Qwen3 GQA group sizes)")
@@ -190,6 +190,63 @@ def bench_stream_ceiling(torch, A, H, HKV, n_layer, ctx, reps=50, seed=1000):
     kv_bytes = 2.0 * ctx * kd * 4
     return {"kernel_ms": ms, "kv_bytes_per_launch": kv_bytes, "gbs": kv_bytes / (ms * 1e-3) / 1e9,
             "decode_bytes_per_launch": A.decode_bytes(ctx, H, HKV)}
+
+
+def bench_project(torch, A, E=2560, H=32, HKV=8, n_layer=36, seed=7000):
+    """The decode step's QKV projection at Qwen3-4B shape (ei_qkv_project: attention RMSNorm + the
+    fused [Wq|Wk|Wv] GEMV, one token): n_layer launches over separate weights in one graph, for fp32
+    and fp16 weights; GB/s of the weight stream + x + out.  Then the whole decode layer from the
+    residual (projection + fused decode step, ctx 4096) per layer."""
+    from exactinfer_amd import _capi
+    dev = "cuda"
+    shape = A.AttnShape(H, HKV)
+    n_out = shape.qkv
+    x = A.synth_fill(torch.empty((n_layer, 1, E), dtype=torch.float32, device=dev), seed)
+    gam = torch.ones((E,), dtype=torch.float32, device=dev)
+    qkv = torch.empty((n_layer, 1, n_out), dtype=torch.float32, device=dev)
+    res = {"workload": f"Qwen3-4B shape: E {E}, {n_out} output rows, one token, {n_layer} layers in one graph"}
+    for wtype, name, esize in ((0, "f32", 4), (1, "f16", 2)):
+        w = torch.empty((n_layer, n_out, E), dtype=torch.float32, device=dev)
+        A.synth_fill(w, seed + 1 + wtype)
+        w.mul_(0.05)
+        if wtype == 1:
+            w = w.to(torch.float16)
+
+        def run():
+            for l in range(n_layer):
+                _capi.call("ei_qkv_project", A._stream(), x[l].data_ptr(), E, 1, E, gam.data_ptr(), 1e-6,
+                           w[l].data_ptr(), wtype, n_out, qkv[l].data_ptr(), n_out)
+
+        ms = graph_ms(torch, run, reps=20, warm=3) / n_layer
+        nbytes = n_out * E * esize + 4.0 * (E + n_out)
+        res[name] = {"kernel_us": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
+                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+        if wtype == 1:  # the decode layer from the residual: projection + fused decode step at ctx 4096
+            ctx = 4096
+            kc = torch.empty((n_layer, ctx, HKV * D), dtype=torch.float32, device=dev)
+            vc = torch.empty_like(kc)
+            for l in range(n_layer):
+                A.synth_fill(kc[l], seed + 10 + 2 * l)
+                A.synth_fill(vc[l], seed + 11 + 2 * l)
+            g2 = torch.ones((2, D), dtype=torch.float32, device=dev)
+            cs = A.rope_table(ctx)
+            pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+            out = torch.empty((n_layer, 1, H, D), dtype=torch.float32, device=dev)
+            ws = [A.DecodeWorkspace(1, H, HKV, ctx) for _ in range(n_layer)]
+
+            def layer_run():
+                for l in range(n_layer):
+                    _capi.call("ei_qkv_project", A._stream(), x[l].data_ptr(), E, 1, E, gam.data_ptr(), 1e-6,
+                               w[l].data_ptr(), wtype, n_out, qkv[l].data_ptr(), n_out)
+                    A.decode_step(qkv[l], kc[l], vc[l], shape, g2[0], g2[1], cs, ws[l], pos_dev=pos, out=out[l])
+
+            ms2 = graph_ms(torch, layer_run, reps=20, warm=3) / n_layer
+            tot = nbytes + A.decode_bytes(ctx, H, HKV)
+            res["decode_layer_from_residual_f16"] = {"us_per_layer": round(ms2 * 1e3, 3), "bytes": tot,
+                                                     "gbs": round(tot / (ms2 * 1e-3) / 1e9, 1)}
+        del w
+    return res
 
 
 def bench_batched(torch, A, steps, warmup, use_graph, seed=3000, block_size=0):
@@ -539,6 +596,10 @@ def main():
         log("stream ceiling of the configs[1] decode plan ...")
         res["stream_ceiling"] = bench_stream_ceiling(torch, A, 32, 8, 36, 4096)
         log(json.dumps(res["stream_ceiling"]))
+    if extra or args.only == "project":
+        log("QKV projection at Qwen3-4B shape ...")
+        res["project"] = bench_project(torch, A)
+        log(json.dumps(res["project"]))
     if extra or args.only == "configs0":
         log("configs[0] on the GPU path ...")
         res["configs0"] = bench_configs0_gpu(torch, A)
@@ -590,7 +651,7 @@ def main():
                                                          "tflops": round(pre["plain_kernel_tflops"], 3)}}}
     # the other configs (parity-test shapes), measured beside the headline for context
     ex = {}
-    for k in ("longctx", "batched", "batched_paged", "prefill_chunked", "stream_ceiling", "configs0"):
+    for k in ("longctx", "batched", "batched_paged", "prefill_chunked", "stream_ceiling", "configs0", "project"):
         if k in res:
             ex[k] = {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in res[k].items()}
             if "gbs" in res[k]:

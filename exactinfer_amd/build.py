@@ -15,7 +15,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libei_attn.so"
-SOURCES = ["csrc/prologue.hip", "csrc/decode.hip", "csrc/prefill.hip", "csrc/capi.cpp", "host/hip_attention.cpp"]
+SOURCES = ["csrc/prologue.hip", "csrc/decode.hip", "csrc/prefill.hip", "csrc/project.hip", "csrc/capi.cpp",
+           "host/hip_attention.cpp"]
 HEADERS = ["common.h", "launch.h"]
 
 HIPCC_FLAGS = [

@@ -437,6 +437,27 @@ EI_API int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, floa
                       "prefill step: attention launch");
 }
 
+EI_API int ei_qkv_project(ei_stream_t stream, const float* x, long x_stride, int rows, int n_embd,
+                          const float* attn_norm, float eps, const void* w, int w_type, int n_out, float* qkv,
+                          long qkv_stride) {
+    REQUIRE(x && attn_norm && w && qkv, "null pointer argument");
+    REQUIRE(w_type == EI_W_F32 || w_type == EI_W_F16, "w_type %d: EI_W_F32 (0) or EI_W_F16 (1)", w_type);
+    if (ei::qkv_project_pieces(n_embd, w_type == EI_W_F16) == 0)
+        return fail(EI_ERR_UNSUPPORTED,
+                    "n_embd %d: built for 1024, 2048, 2560, 4096 and 5120 (F32) and also 8192 and 10240 (F16)", n_embd);
+    REQUIRE(rows >= 0 && rows <= ei::qkv_project_max_rows(n_embd), "rows %d: at most %d rows per launch at n_embd %d",
+            rows, ei::qkv_project_max_rows(n_embd), n_embd);
+    REQUIRE(n_out > 0, "n_out %d", n_out);
+    REQUIRE(x_stride >= n_embd && qkv_stride >= n_out, "x_stride %ld / qkv_stride %ld too small", x_stride,
+            qkv_stride);
+    REQUIRE(aligned16(x) && aligned16(w) && aligned16(attn_norm) && x_stride % 4 == 0,
+            "x, w, attn_norm and x_stride must be 16-byte aligned");
+    if (rows == 0) return ok();
+    return hip_status(ei::launch_qkv_project(static_cast<hipStream_t>(stream), x, x_stride, rows, n_embd, attn_norm,
+                                             eps, w, w_type == EI_W_F16, n_out, qkv, qkv_stride),
+                      "qkv projection launch");
+}
+
 EI_API int ei_stream_ceiling(ei_stream_t stream, const float* kc, const float* vc, int n_head_kv, int kv_len,
                              float* sink) {
     REQUIRE(kc && vc && sink, "null pointer argument");

@@ -89,6 +89,14 @@ hipError_t launch_stream_ceiling(hipStream_t st, const float* kc, const float* v
 constexpr size_t kDecodeScratchBytes = size_t(4) << 20;
 hipError_t decode_scratch(void** ptr);
 
+// ------------------------------------------------------------------ project.hip
+// attention RMSNorm of B activation rows + the fused QKV product (raw [Q|K|V] rows out)
+constexpr int kProjMaxRows = 4;
+int qkv_project_max_rows(int E);                // rows per launch at hidden size E
+int qkv_project_pieces(int E, bool w_f16);      // 0 when hidden size E is not built
+hipError_t launch_qkv_project(hipStream_t st, const float* x, long x_stride, int B, int E, const float* gamma,
+                              float eps, const void* w, bool w_f16, int n_out, float* out, long out_stride);
+
 // ------------------------------------------------------------------ prefill.hip
 // Key split across workgroups for short chunks: ksplit shares per query block, merged by a
 // second launch; fixed by (B, max_kv) so graphs replay unchanged.

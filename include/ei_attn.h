@@ -53,6 +53,23 @@ int ei_abi_version(void);
  * The caller copies it to device memory once. */
 int ei_rope_table_fill(float* cs_host, int n_ctx, int rope_dim, double theta);
 
+/* ------------------------------------------------------------------ QKV projection
+ * Weight element types of ei_qkv_project (the GGML type ids of F32 and F16). */
+enum { EI_W_F32 = 0, EI_W_F16 = 1 };
+
+/* Attention RMSNorm + fused QKV projection of `rows` activation rows (decode: one token per
+ * sequence): h = rmsnorm(x_b, attn_norm, eps) (sum of squares in double, as the CPU rmsnorm),
+ * then qkv_b[r] = sum_i W[r][i] h[i] for the n_out = (n_head + 2 n_head_kv) * 128 rows of the
+ * fused [Wq | Wk | Wv] weight (row r of n_embd contiguous elements, F32 or F16 as w_type).
+ * Row b of x at x + b*x_stride, of qkv at qkv + b*qkv_stride, left raw: the decode steps
+ * (ei_decode_step, ei_decode_step_paged) apply the QK-norm, RoPE and cache append to it.
+ * Replaces k_rmsnorm + linear(h, L.qkv, qkv, ...) of src/cuda/model_cuda.cu:1797-1799 (the
+ * B == 1 GEMV, :300-320); arithmetic of the CPU path's rmsnorm + matvec (src/ops.cpp:126-160).
+ * Built for n_embd 1024, 2048, 2560, 4096, 5120 (every dense Qwen3; F16 also 8192, 10240);
+ * 0 <= rows <= min(4, 24576 / n_embd). */
+int ei_qkv_project(ei_stream_t stream, const float* x, long x_stride, int rows, int n_embd, const float* attn_norm,
+                   float eps, const void* w, int w_type, int n_out, float* qkv, long qkv_stride);
+
 /* ------------------------------------------------------------------ QK-norm + RoPE
  * In place on `rows` rows of `buf` (row b at buf + b*row_stride, head h at + h*128):
  * per head, RMSNorm with gamma (sum of squares in double, inv = float(1/sqrt(ss/128+eps)),

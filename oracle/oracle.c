@@ -27,6 +27,10 @@
  *   orc_attn_split_combine  == single-pass orc_attn_decode within fp32 tolerance, and
  *                        float64 brute force; empty-split rule.
  *   orc_attn_f64         textbook softmax attention in double; checked by the closed forms.
+ *   orc_f16_to_f32,      bit-exact vs the reference's own f16_to_f32, dot_f32 and dot_f16
+ *   orc_dot_f32,         (src/ops.cpp:22-24, :92-118) compiled from source (oracle/_ref),
+ *   orc_dot_f16          on every binary16 pattern and on dot lengths with and without
+ *                        tails; orc_matvec + float64 bound.
  *   orc_fill_normal      synthetic-input generator (not a reference function): exact
  *                        integer arithmetic, checked for moments and against the GPU fill.
  */
@@ -291,6 +295,82 @@ ORC_API void orc_attn_split_combine(const float* q, const float* kc, const float
     free(pacc);
     free(pm);
     free(pl);
+}
+
+/* ------------------------------------------------------------------ QKV projection (matvec)
+ * binary16 -> binary32, exact (what _mm_cvtph_ps does in f16_to_f32, src/ops.cpp:22-24):
+ * normals rebias the exponent, subnormals are normalised, inf/NaN keep their payload. */
+ORC_API float orc_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu, bits;
+    if (exp == 0x1Fu) {
+        bits = sign | 0x7F800000u | (man << 13);
+    } else if (exp != 0) {
+        bits = sign | ((exp + 112u) << 23) | (man << 13);
+    } else if (man == 0) {
+        bits = sign;
+    } else {  /* subnormal: value man * 2^-24 */
+        int e = -1;
+        do {
+            man <<= 1;
+            ++e;
+        } while (!(man & 0x400u));
+        bits = sign | ((uint32_t)(112 - e) << 23) | ((man & 0x3FFu) << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* hsum of an 8-lane float vector in the order of src/ops.cpp:84-90:
+ * ((v0+v4) + (v2+v6)) + ((v1+v5) + (v3+v7)). */
+static float orc_hsum8(const float* v) {
+    float lo[4];
+    for (int i = 0; i < 4; ++i) lo[i] = v[i] + v[i + 4];
+    const float a = lo[0] + lo[2], b = lo[1] + lo[3];
+    return a + b;
+}
+
+/* dot_f32 (src/ops.cpp:108-118): lanes k of two 8-wide FMA accumulators take elements
+ * j+k and j+8+k of each 16-element block; then hsum(a0 + a1), then the scalar tail. */
+ORC_API float orc_dot_f32(const float* w, const float* x, long n) {
+    float a0[8] = {0}, a1[8] = {0}, v[8];
+    long j = 0;
+    for (; j + 16 <= n; j += 16)
+        for (int k = 0; k < 8; ++k) {
+            a0[k] = fmaf(w[j + k], x[j + k], a0[k]);
+            a1[k] = fmaf(w[j + 8 + k], x[j + 8 + k], a1[k]);
+        }
+    for (int k = 0; k < 8; ++k) v[k] = a0[k] + a1[k];
+    float s = orc_hsum8(v);
+    for (; j < n; ++j) s += w[j] * x[j];
+    return s;
+}
+
+/* dot_f16 (src/ops.cpp:92-106): four 8-wide FMA accumulators over 32-element blocks, then
+ * 8-element blocks into a0; hsum((a0 + a1) + (a2 + a3)); the scalar tail converts each
+ * weight and adds its product. */
+ORC_API float orc_dot_f16(const uint16_t* w, const float* x, long n) {
+    float a[4][8] = {{0}}, v[8];
+    long j = 0;
+    for (; j + 32 <= n; j += 32)
+        for (int u = 0; u < 4; ++u)
+            for (int k = 0; k < 8; ++k)
+                a[u][k] = fmaf(orc_f16_to_f32(w[j + 8 * u + k]), x[j + 8 * u + k], a[u][k]);
+    for (; j + 8 <= n; j += 8)
+        for (int k = 0; k < 8; ++k) a[0][k] = fmaf(orc_f16_to_f32(w[j + k]), x[j + k], a[0][k]);
+    for (int k = 0; k < 8; ++k) v[k] = (a[0][k] + a[1][k]) + (a[2][k] + a[3][k]);
+    float s = orc_hsum8(v);
+    for (; j < n; ++j) s += orc_f16_to_f32(w[j]) * x[j];
+    return s;
+}
+
+/* matvec for F32 (type 0) and F16 (type 1) weights (src/ops.cpp:126-153): y[r] = row r . x,
+ * rows of n elements stored one after another (GGUF ne[0] = n is the contiguous dimension). */
+ORC_API void orc_matvec(int type, const void* w, const float* x, float* y, long rows, long n) {
+#pragma omp parallel for schedule(static)
+    for (long r = 0; r < rows; ++r)
+        y[r] = type == 0 ? orc_dot_f32((const float*)w + r * n, x, n) : orc_dot_f16((const uint16_t*)w + r * n, x, n);
 }
 
 /* ------------------------------------------------------------------ float64 brute force

@@ -21,6 +21,7 @@ _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
 _c_int, _c_long, _c_float, _c_double = ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_double
 _c_size, _c_u64 = ctypes.c_size_t, ctypes.c_uint64
 
@@ -58,6 +59,13 @@ def lib():
         L.orc_attn_split_combine.argtypes = [_f32p, _f32p, _f32p, _f32p, _c_int, _c_int, _c_int, _c_int, _c_float,
                                              _c_int]
         L.orc_attn_f64.argtypes = [_f32p, _f32p, _f32p, _f64p, _c_int, _c_int, _c_int, _c_int, _c_double]
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_f16_to_f32.restype = _c_float
+        L.orc_dot_f32.argtypes = [_f32p, _f32p, _c_long]
+        L.orc_dot_f32.restype = _c_float
+        L.orc_dot_f16.argtypes = [_u16p, _f32p, _c_long]
+        L.orc_dot_f16.restype = _c_float
+        L.orc_matvec.argtypes = [_c_int, ctypes.c_void_p, _f32p, _f32p, _c_long, _c_long]
         L.orc_threads.restype = _c_int
         L.orc_set_threads.argtypes = [_c_int]
         _lib = L
@@ -72,6 +80,13 @@ def ref_lib():
         R.elref_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _c_int, _c_float]
         R.elref_rope_inv_freq.argtypes = [_f64p, _c_int, _c_double]
         R.elref_rope.argtypes = [_f32p, _c_int, _c_int, _f64p]
+        if hasattr(R, "elref_dot_f32"):
+            R.elref_f16_to_f32.argtypes = [ctypes.c_uint16]
+            R.elref_f16_to_f32.restype = _c_float
+            R.elref_dot_f32.argtypes = [_f32p, _f32p, _c_long]
+            R.elref_dot_f32.restype = _c_float
+            R.elref_dot_f16.argtypes = [_u16p, _f32p, _c_long]
+            R.elref_dot_f16.restype = _c_float
         _ref = R
     return _ref
 
@@ -196,3 +211,39 @@ def set_threads(n: int) -> None:
 def env_threads() -> int:
     v = os.environ.get("OMP_NUM_THREADS")
     return int(v) if v and v.isdigit() else (os.cpu_count() or 1)
+
+
+# ---------------------------------------------------------------- QKV projection
+W_F32, W_F16 = 0, 1
+
+
+def f16_to_f32(h) -> np.ndarray:
+    """binary16 bit patterns -> float32, exact (src/ops.cpp:22-24)."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    L = lib()
+    return np.array([L.orc_f16_to_f32(int(v)) for v in h.reshape(-1)], np.float32).reshape(h.shape)
+
+
+def dot(w, x, wtype: int) -> float:
+    """dot_f32 / dot_f16 of src/ops.cpp:92-118 (w float32, or uint16 binary16 patterns)."""
+    x = _c(x)
+    if wtype == W_F32:
+        return float(lib().orc_dot_f32(_c(w), x, x.size))
+    return float(lib().orc_dot_f16(np.ascontiguousarray(w, dtype=np.uint16), x, x.size))
+
+
+def matvec(w, x, wtype: int) -> np.ndarray:
+    """y = W x for W [rows][n] (src/ops.cpp:126-153): float32 weights (W_F32) or binary16
+    patterns as uint16 (W_F16)."""
+    w = np.ascontiguousarray(w, dtype=np.float32 if wtype == W_F32 else np.uint16)
+    x = _c(x)
+    rows, n = w.shape
+    y = np.empty(rows, np.float32)
+    lib().orc_matvec(wtype, w.ctypes.data, x, y, rows, n)
+    return y
+
+
+def rmsnorm_rows(x, w, eps=1e-6):
+    """src/ops.cpp:155-160 on every row of x [B][n]."""
+    x = np.atleast_2d(_c(x))
+    return np.stack([rmsnorm(r, w, eps) for r in x])

@@ -6,11 +6,15 @@
 //   elref_rope_inv_freq  -> el::rope_inv_freq  (src/model.cpp:105-109)
 //   elref_rope           -> el::rope           (src/model.cpp:23-32; file-local, hence the
 //                                                include of model.cpp into this unit)
+//   elref_f16_to_f32     -> el::f16_to_f32     (src/ops.cpp:22-24)
+//   elref_dot_f32        -> dot_f32            (src/ops.cpp:108-118; file-local, hence the
+//   elref_dot_f16        -> dot_f16             include of ops.cpp into this unit, :92-106)
 //
 // Everything else in those files (CpuModel, read_config, the GGUF tensor table) is left
 // unreferenced and dropped by --gc-sections: it needs src/gguf.cpp, which includes
 // <windows.h> and does not build here.
 #include "model.cpp"
+#include "ops.cpp"
 #include "ops.h"
 
 #define REF_API extern "C" __attribute__((visibility("default")))
@@ -31,3 +35,9 @@ REF_API void elref_rope(float* v, int pos, int dim, const double* inv_freq) {
     const std::vector<double> f(inv_freq, inv_freq + dim / 2);
     el::rope(v, pos, dim, f);
 }
+
+REF_API float elref_f16_to_f32(uint16_t h) { return el::f16_to_f32(h); }
+
+REF_API float elref_dot_f32(const float* w, const float* x, long n) { return el::dot_f32(w, x, n); }
+
+REF_API float elref_dot_f16(const uint16_t* w, const float* x, long n) { return el::dot_f16(w, x, n); }

@@ -8,6 +8,9 @@ compiled from its sources by oracle/Makefile).
                         reference's code, checked against the oracle in tests/test_oracle.py.
   attn_small.npz        seeded small attention cases with the float64 brute-force output
                         (orc_attn_f64): a regression anchor for the oracle's attention.
+  ref_matvec.npz        inputs and outputs of the reference's dot_f32 / dot_f16 (src/ops.cpp:92-118,
+                        compiled from source) on seeded rows of lengths with and without tails, and
+                        of its f16_to_f32 on every binary16 pattern (as a checksum of the bits).
 
     python tests/golden/make_golden.py
 """
@@ -61,6 +64,24 @@ def main():
         cases[f"{name}_shape"] = np.array([H, HKV, T], dtype=np.int32)
         cases[f"{name}_seeds"] = np.array([300 + T, 100 + T, 200 + T], dtype=np.int64)  # q, k, v
     np.savez_compressed(HERE / "attn_small.npz", **cases)
+
+    mv = {}
+    rng = np.random.default_rng(8000)
+    for n in (7, 8, 16, 31, 32, 37, 128, 2560, 2571):
+        x = O.normal((n,), 8100 + n)
+        w32 = O.normal((n,), 8200 + n)
+        # binary16 weights spanning normals, subnormals and both signs
+        w16 = rng.integers(0, 0x7C00, n).astype(np.uint16) | (rng.integers(0, 2, n).astype(np.uint16) << 15)
+        mv[f"x_{n}"] = x
+        mv[f"w32_{n}"] = w32
+        mv[f"w16_{n}"] = w16
+        mv[f"dot32_{n}"] = np.array([R.elref_dot_f32(w32, x, n)], np.float32)
+        mv[f"dot16_{n}"] = np.array([R.elref_dot_f16(w16, x, n)], np.float32)
+    allh = np.arange(1 << 16, dtype=np.uint32)
+    conv = np.array([R.elref_f16_to_f32(int(h)) for h in allh], np.float32)
+    # NaN payloads compare by bits; the checksum covers every pattern's converted bits
+    mv["f16_all_bits_sum"] = np.array([int(conv.view(np.uint32).astype(np.uint64).sum())], np.uint64)
+    np.savez_compressed(HERE / "ref_matvec.npz", **mv)
     print("wrote", sorted(p.name for p in HERE.glob("*.npz")))
 
 

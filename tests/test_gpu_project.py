@@ -1,0 +1,124 @@
+"""GPU parity of the QKV projection (ei_qkv_project): attention RMSNorm + the fused [Wq|Wk|Wv]
+product against the oracle's restatement of the CPU path (rmsnorm, src/ops.cpp:155-160, then
+matvec with dot_f32 / dot_f16, src/ops.cpp:92-153; the oracle's dot products are bit-exact with
+the reference's own, tests/test_oracle.py).  The sum order differs (a wave tree of per-lane FMA
+chains against the reference's 8-lane AVX2 accumulators), so every output must lie within
+1e-5 of sum_i |w_i h_i| (float64) of the reference: a dropped or repeated block of 16 terms
+moves an output by ~1/160 of that scale.  Then the decode layer from the residual stream:
+x -> ei_qkv_project -> ei_decode_step, its cache append bit-exact against the oracle applied to
+the projected row and its attention within the 1e-5 attention bar."""
+import numpy as np
+import pytest
+
+from tests.parity import ATTN_RTOL, bits_equal, gate
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+W_F32, W_F16 = 0, 1
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def _project(gpu, x, gamma, w, wtype, n_out, eps=1e-6):
+    import torch
+    from exactinfer_amd import _capi
+    rows, E = x.shape
+    out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    xd, gd, wd = _dev(x), _dev(gamma), _dev(w)
+    _capi.call("ei_qkv_project", gpu._stream(), xd.data_ptr(), E, rows, E, gd.data_ptr(), float(eps), wd.data_ptr(),
+               wtype, n_out, out.data_ptr(), n_out)
+    return out
+
+
+def _weights(orc, n_out, E, wtype, seed):
+    w = orc.normal((n_out, E), seed) * np.float32(0.05)
+    return w if wtype == W_F32 else w.astype(np.float16).view(np.uint16)
+
+
+def _wf(w, wtype):
+    return (w if wtype == W_F32 else w.view(np.float16)).astype(np.float64)
+
+
+@pytest.mark.parametrize("wtype", [W_F32, W_F16])
+@pytest.mark.parametrize("E,H,HKV,rows", [(2560, 32, 8, 1), (2560, 32, 8, 4), (1024, 16, 8, 1), (2048, 16, 8, 3),
+                                         (4096, 32, 8, 2), (5120, 40, 8, 1)])
+def test_qkv_project_matches_oracle(orc, gpu, wtype, E, H, HKV, rows):
+    n_out = (H + 2 * HKV) * D
+    x = orc.normal((rows, E), 8500 + E) * np.float32(3.0)
+    gamma = orc.gamma(E, 8501)
+    w = _weights(orc, n_out, E, wtype, 8502 + E)
+    got = _host(_project(gpu, x, gamma, w, wtype, n_out))
+    for b in range(rows):
+        h = orc.rmsnorm(x[b], gamma)
+        ref = orc.matvec(w, h, wtype)
+        mag = np.abs(_wf(w, wtype)) @ np.abs(h.astype(np.float64))
+        err = np.max(np.abs(got[b].astype(np.float64) - ref) / mag)
+        assert err <= 1e-5, f"row {b}: max |got - ref| / sum|w h| = {err:.3e}"
+        exact = _wf(w, wtype) @ h.astype(np.float64)
+        assert np.max(np.abs(got[b] - exact) / mag) <= 1e-5
+
+
+def test_qkv_project_rejects_unbuilt_shapes(gpu):
+    import ctypes
+    from exactinfer_amd import _capi
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    with pytest.raises(_capi.EiError, match="n_embd 3000"):
+        _capi.call("ei_qkv_project", None, p, 3000, 1, 3000, p, 1e-6, p, W_F32, 6144, p, 6144)
+    with pytest.raises(_capi.EiError, match="rows 5"):
+        _capi.call("ei_qkv_project", None, p, 2560, 5, 2560, p, 1e-6, p, W_F32, 6144, p, 6144)
+    with pytest.raises(_capi.EiError, match="w_type"):
+        _capi.call("ei_qkv_project", None, p, 2560, 1, 2560, p, 1e-6, p, 7, 6144, p, 6144)
+
+
+@pytest.mark.parametrize("wtype", [W_F32, W_F16])
+def test_decode_layer_from_residual(orc, gpu, wtype):
+    """Qwen3-4B shapes: residual x -> attention RMSNorm + QKV projection -> fused decode step."""
+    E, H, HKV, T = 2560, 32, 8, 1000
+    shape = gpu.AttnShape(H, HKV)
+    n_out = shape.qkv
+    x = orc.normal((1, E), 8600)
+    gamma = orc.gamma(E, 8601)
+    w = _weights(orc, n_out, E, wtype, 8602)
+    qg, kg = orc.gamma(D, 8603), orc.gamma(D, 8604)
+    k, v = orc.normal((T, HKV * D), 8605), orc.normal((T, HKV * D), 8606)
+    kc, vc = _dev(k), _dev(v)
+    cs = gpu.rope_table(T)
+    ws = gpu.DecodeWorkspace(1, H, HKV, T)
+    qkv = _project(gpu, x, gamma, w, wtype, n_out)
+    import torch
+    pos = torch.tensor([T - 1], dtype=torch.int32, device="cuda")
+    out = _host(gpu.decode_step(qkv, kc, vc, shape, _dev(qg), _dev(kg), cs, ws, pos_dev=pos))
+    # stage 2 against the oracle applied to the projected row itself
+    row = _host(qkv)
+    normed = orc.headnorm_rope(row, H, D, qg, T - 1, 128, 1e6, 1e-6)
+    normed = orc.headnorm_rope(normed, HKV, D, kg, T - 1, 128, 1e6, 1e-6, col0=H * D)
+    rk, rv = k.copy(), v.copy()
+    orc.kv_append(normed[:, H * D:(H + HKV) * D], normed[:, (H + HKV) * D:], rk, rv, T - 1)
+    assert bits_equal(_host(kc), rk) and bits_equal(_host(vc), rv)
+    qn = np.ascontiguousarray(normed[0, :H * D].reshape(H, D))
+    kk, vv = rk.reshape(T, HKV, D), rv.reshape(T, HKV, D)
+    ok, msg = gate(f"decode layer from residual w_type {wtype}", out.reshape(H, D),
+                   orc.attn_decode(qn, kk, vv, T, H, HKV, D), lambda: orc.attn_f64(qn, kk, vv, T, H, HKV, D))
+    assert ok, msg
+    # and the whole chain against the oracle chain (rmsnorm -> matvec -> QK-norm/RoPE -> attention):
+    # the projection's different sum order moves q and k by ~1e-6, so the bar is looser here
+    h = orc.rmsnorm(x[0], gamma)
+    qkv_ref = orc.matvec(w, h, wtype)[None]
+    nr = orc.headnorm_rope(qkv_ref, H, D, qg, T - 1, 128, 1e6, 1e-6)
+    nr = orc.headnorm_rope(nr, HKV, D, kg, T - 1, 128, 1e6, 1e-6, col0=H * D)
+    rk2, rv2 = k.copy(), v.copy()
+    orc.kv_append(nr[:, H * D:(H + HKV) * D], nr[:, (H + HKV) * D:], rk2, rv2, T - 1)
+    ref_chain = orc.attn_decode(np.ascontiguousarray(nr[0, :H * D].reshape(H, D)), rk2.reshape(T, HKV, D),
+                                rv2.reshape(T, HKV, D), T, H, HKV, D)
+    from tests.parity import rel_err
+    assert rel_err(out.reshape(H, D), ref_chain) <= 20 * ATTN_RTOL

@@ -264,3 +264,64 @@ def test_oracle_attention_regression_fixture(orc):
         q, k, v = orc.normal((H, D), sq), orc.normal((T, HKV, D), sk), orc.normal((T, HKV, D), sv)
         out = orc.attn_decode(q, k, v, T, H, HKV, D)
         assert rel_err(out, a[f"{name}_f64"]) <= ATTN_RTOL
+
+
+# ---------------------------------------------------------------- QKV projection (matvec)
+def test_f16_conversion_matches_reference_on_every_pattern(orc):
+    """orc_f16_to_f32 == the reference's f16_to_f32 (src/ops.cpp:22-24) on all 65536 binary16
+    patterns: directly where oracle/_ref builds, and through the committed bit checksum."""
+    allh = np.arange(1 << 16, dtype=np.uint16)
+    conv = orc.f16_to_f32(allh)
+    # numpy's binary16 -> binary32 conversion is exact too (NaNs compared by bits below)
+    ref_np = allh.view(np.float16).astype(np.float32)
+    finite = np.isfinite(ref_np)
+    assert bits_equal(conv[finite], ref_np[finite])
+    assert np.all(np.isnan(conv[~np.isfinite(ref_np) & np.isnan(ref_np)]))
+    g = np.load(GOLDEN / "ref_matvec.npz")
+    assert int(conv.view(np.uint32).astype(np.uint64).sum()) == int(g["f16_all_bits_sum"][0])
+    R = orc.ref_lib()
+    if R is not None and hasattr(R, "elref_f16_to_f32"):
+        got = np.array([R.elref_f16_to_f32(int(h)) for h in allh[::97]], np.float32)
+        assert bits_equal(got, conv[::97])
+
+
+def test_dot_products_match_reference_golden_vectors(orc):
+    """orc_dot_f32 / orc_dot_f16 reproduce the reference's dot_f32 / dot_f16 (src/ops.cpp:92-118,
+    AVX2 FMA accumulators and hsum order) bit for bit, with and without scalar tails."""
+    g = np.load(GOLDEN / "ref_matvec.npz")
+    for n in (7, 8, 16, 31, 32, 37, 128, 2560, 2571):
+        x, w32, w16 = g[f"x_{n}"], g[f"w32_{n}"], g[f"w16_{n}"]
+        assert bits_equal(np.float32(orc.dot(w32, x, orc.W_F32)), g[f"dot32_{n}"][0]), f"dot_f32 n={n}"
+        assert bits_equal(np.float32(orc.dot(w16, x, orc.W_F16)), g[f"dot16_{n}"][0]), f"dot_f16 n={n}"
+
+
+def test_dot_products_match_reference_built_from_source(orc):
+    R = orc.ref_lib()
+    if R is None or not hasattr(R, "elref_dot_f32"):
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    rng = np.random.default_rng(9)
+    for n in (1, 9, 15, 17, 33, 63, 65, 1000, 4096, 4099):
+        x = orc.normal((n,), 9100 + n) * np.float32(rng.uniform(0.01, 100))
+        w32 = orc.normal((n,), 9200 + n)
+        w16 = np.float32(rng.standard_normal(n)).astype(np.float16).view(np.uint16)
+        assert bits_equal(np.float32(orc.dot(w32, x, orc.W_F32)), np.float32(R.elref_dot_f32(w32, x, n)))
+        assert bits_equal(np.float32(orc.dot(w16, x, orc.W_F16)), np.float32(R.elref_dot_f16(w16, x, n)))
+
+
+def test_matvec_is_the_float64_product_within_fp32_rounding(orc):
+    """Independent of the summation order: |y - W x (float64)| <= 1e-6 * sum |w_i x_i| per row, and a
+    dropped or doubled term (an off-by-one in the block loops) would far exceed it."""
+    rows, n = 64, 2560
+    x = orc.normal((n,), 9300)
+    w = orc.normal((rows, n), 9301)
+    y = orc.matvec(w, x, orc.W_F32)
+    exact = w.astype(np.float64) @ x.astype(np.float64)
+    mag = np.abs(w.astype(np.float64)) @ np.abs(x.astype(np.float64))
+    assert np.all(np.abs(y - exact) <= 1e-6 * mag)
+    w16 = w.astype(np.float16)
+    y16 = orc.matvec(w16.view(np.uint16), x, orc.W_F16)
+    exact16 = w16.astype(np.float64) @ x.astype(np.float64)
+    assert np.all(np.abs(y16 - exact16) <= 1e-6 * mag)
+    # the same bound rejects a matvec missing its last block
+    bad = (w[:, :-16].astype(np.float64) @ x[:-16].astype(np.float64))
+    assert np.any(np.abs(bad - exact) > 1e-6 * mag)
