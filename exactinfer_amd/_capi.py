@@ -21,6 +21,9 @@ EXPORTS = (
     "ei_last_error", "ei_abi_version", "ei_rope_table_fill", "ei_headnorm_rope", "ei_kv_append", "ei_qkv_prepare",
     "ei_attn_decode_ws_bytes", "ei_attn_workspace_init", "ei_attn_decode", "ei_attn_decode_batched",
     "ei_decode_step", "ei_decode_step_noalloc", "ei_attn_decode_paged", "ei_decode_step_paged", "ei_attn_prefill", "ei_attn_prefill_ws_bytes", "ei_attn_prefill_split", "ei_prefill_step", "ei_qkv_project", "ei_stream_ceiling", "ei_synth_fill",
+    # include/ei_gguf.h
+    "ei_gguf_open", "ei_gguf_close", "ei_gguf_version", "ei_gguf_n_tensors", "ei_gguf_tensor", "ei_gguf_find_tensor",
+    "ei_gguf_get_int", "ei_gguf_get_float", "ei_gguf_get_str", "ei_gguf_qwen3_config",
 )
 
 _vp, _i, _l, _f, _d, _sz, _u64 = (ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_double,
@@ -49,6 +52,16 @@ _SIGS = {
     "ei_attn_prefill_split": ([_vp, _vp, _l, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp, _sz], _i),
     "ei_prefill_step": ([_vp, _vp, _l, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _i, _f, _f, _i, _vp, _sz], _i),
     "ei_qkv_project": ([_vp, _vp, _l, _i, _i, _vp, _f, _vp, _i, _i, _vp, _l], _i),
+    "ei_gguf_open": ([ctypes.c_char_p], _vp),
+    "ei_gguf_close": ([_vp], None),
+    "ei_gguf_version": ([_vp], _i),
+    "ei_gguf_n_tensors": ([_vp], _l),
+    "ei_gguf_tensor": ([_vp, _l, _vp, _vp, _vp, _vp, _vp, _vp], _i),
+    "ei_gguf_find_tensor": ([_vp, ctypes.c_char_p], _l),
+    "ei_gguf_get_int": ([_vp, ctypes.c_char_p, _vp], _i),
+    "ei_gguf_get_float": ([_vp, ctypes.c_char_p, _vp], _i),
+    "ei_gguf_get_str": ([_vp, ctypes.c_char_p, _vp], _i),
+    "ei_gguf_qwen3_config": ([_vp, _vp], _i),
     "ei_stream_ceiling": ([_vp, _vp, _vp, _i, _i, _vp], _i),
     "ei_synth_fill": ([_vp, _vp, _sz, _u64, _u64, _l, _l, _f], _i),
 }

@@ -10,6 +10,8 @@
 #include <string>
 
 #include "../../include/ei_attn.h"
+#include "../../include/ei_gguf.h"
+#include "../host/gguf.h"
 #include "launch.h"
 
 namespace {
@@ -474,4 +476,112 @@ EI_API int ei_synth_fill(ei_stream_t stream, float* dst, size_t n, uint64_t seed
     return hip_status(ei::launch_synth_fill(static_cast<hipStream_t>(stream), dst, n, seed, offset, row_len,
                                             spike_every, spike_mult),
                       "synth fill launch");
+}
+
+// ------------------------------------------------------------------ GGUF reader (include/ei_gguf.h)
+struct ei_gguf {
+    ei::GgufFile file;
+    explicit ei_gguf(const char* path) : file(path) {}
+};
+
+EI_API ei_gguf* ei_gguf_open(const char* path) {
+    if (!path) {
+        fail(EI_ERR_ARG, "path is null");
+        return nullptr;
+    }
+    try {
+        ei_gguf* g = new ei_gguf(path);
+        ok();
+        return g;
+    } catch (const std::exception& e) {
+        fail(EI_ERR_ARG, "%s", e.what());
+    } catch (...) {
+        fail(EI_ERR_ARG, "unknown error reading %s", path);
+    }
+    return nullptr;
+}
+
+EI_API void ei_gguf_close(ei_gguf* g) { delete g; }
+
+EI_API int ei_gguf_version(const ei_gguf* g) { return g ? (int)g->file.version() : 0; }
+
+EI_API long ei_gguf_n_tensors(const ei_gguf* g) { return g ? (long)g->file.tensors().size() : 0; }
+
+EI_API int ei_gguf_tensor(const ei_gguf* g, long index, const char** name, int* type, int* n_dims, uint64_t* ne,
+                          const void** data, uint64_t* nbytes) {
+    REQUIRE(g != nullptr, "file handle is null");
+    REQUIRE(index >= 0 && index < (long)g->file.tensors().size(), "tensor index %ld out of range", index);
+    const ei::GgufTensor& t = g->file.tensors()[(size_t)index];
+    if (name) *name = t.name.c_str();
+    if (type) *type = (int)t.type;
+    if (n_dims) *n_dims = (int)t.ne.size();
+    if (ne)
+        for (size_t i = 0; i < 4; ++i) ne[i] = i < t.ne.size() ? t.ne[i] : 1;
+    if (data) *data = t.data;
+    if (nbytes) *nbytes = t.nbytes;
+    return ok();
+}
+
+EI_API long ei_gguf_find_tensor(const ei_gguf* g, const char* name) {
+    if (!g || !name) return -1;
+    const ei::GgufTensor* t = g->file.tensor(name);
+    return t ? (long)(t - g->file.tensors().data()) : -1;
+}
+
+namespace {
+
+template <class F>
+int gguf_call(const ei_gguf* g, const char* key, F f) {
+    REQUIRE(g != nullptr && key != nullptr, "null argument");
+    try {
+        f();
+        return ok();
+    } catch (const std::exception& e) {
+        return fail(EI_ERR_ARG, "%s", e.what());
+    }
+}
+
+}  // namespace
+
+EI_API int ei_gguf_get_int(const ei_gguf* g, const char* key, int64_t* out) {
+    return gguf_call(g, key, [&] {
+        const int64_t v = g->file.get_int(key);
+        if (out) *out = v;
+    });
+}
+
+EI_API int ei_gguf_get_float(const ei_gguf* g, const char* key, double* out) {
+    return gguf_call(g, key, [&] {
+        const double v = g->file.get_float(key);
+        if (out) *out = v;
+    });
+}
+
+EI_API int ei_gguf_get_str(const ei_gguf* g, const char* key, const char** out) {
+    return gguf_call(g, key, [&] {
+        const std::string& v = g->file.get_str(key);
+        if (out) *out = v.c_str();
+    });
+}
+
+EI_API int ei_gguf_qwen3_config(const ei_gguf* g, ei_qwen3_config* out) {
+    REQUIRE(g != nullptr && out != nullptr, "null argument");
+    try {
+        ei::Qwen3Config c = ei::qwen3_config(g->file);
+        (void)ei::qwen3_tensors(g->file, c);
+        out->n_layer = c.n_layer;
+        out->n_embd = c.n_embd;
+        out->n_ff = c.n_ff;
+        out->n_head = c.n_head;
+        out->n_head_kv = c.n_head_kv;
+        out->head_dim = c.head_dim;
+        out->rope_dim = c.rope_dim;
+        out->n_ctx_train = c.n_ctx_train;
+        out->n_vocab = c.n_vocab;
+        out->rope_base = c.rope_base;
+        out->eps = c.eps;
+        return ok();
+    } catch (const std::exception& e) {
+        return fail(EI_ERR_ARG, "%s", e.what());
+    }
 }

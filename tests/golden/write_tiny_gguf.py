@@ -1,0 +1,115 @@
+"""Writes a tiny synthetic Qwen3 model as a GGUF file (test infrastructure).
+
+No Qwen3 GGUF exists in this environment, so the reader and the end-to-end harness are exercised
+on files this script writes from tests/tiny_qwen3.py's seeded random weights: the tensor names,
+shapes and metadata keys a Qwen3 GGUF carries (read_config / read_tensors, src/model.cpp:38-103),
+F32 or F16 weights (norm vectors stay F32), GGUF version 3, the data section aligned to
+general.alignment.  The writer is independent of the reader under test (plain struct packing).
+
+    python tests/golden/write_tiny_gguf.py OUT.gguf [--f16] [--seed N]
+"""
+from __future__ import annotations
+
+import argparse
+import struct
+import sys
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent.parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+T_U32, T_I32, T_F32, T_STRING, T_U64, T_F64 = 4, 5, 6, 8, 10, 12
+
+
+def _s(x: str) -> bytes:
+    b = x.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def _kv(key: str, t: int, value) -> bytes:
+    out = _s(key) + struct.pack("<I", t)
+    if t == T_STRING:
+        return out + _s(value)
+    fmt = {T_U32: "<I", T_I32: "<i", T_F32: "<f", T_U64: "<Q", T_F64: "<d"}[t]
+    return out + struct.pack(fmt, value)
+
+
+def qwen3_tensors(model, f16: bool) -> list[tuple[str, np.ndarray]]:
+    """(GGUF name, array with ne[0] as its last axis) in file order; matrices F16 when f16."""
+    D = 128
+    mat = (lambda a: np.ascontiguousarray(a, dtype=np.float16)) if f16 else (
+        lambda a: np.ascontiguousarray(a, dtype=np.float32))
+    vec = lambda a: np.ascontiguousarray(a, dtype=np.float32)
+    QD, KD = model.H * D, model.HKV * D
+    out = [("token_embd.weight", mat(model.emb)), ("output_norm.weight", vec(model.out_norm)),
+           ("output.weight", mat(model.lm))]
+    for l, L in enumerate(model.layers):
+        b = f"blk.{l}."
+        out += [(b + "attn_norm.weight", vec(L["attn_norm"])),
+                (b + "attn_q.weight", mat(L["wqkv"][:QD])),
+                (b + "attn_k.weight", mat(L["wqkv"][QD:QD + KD])),
+                (b + "attn_v.weight", mat(L["wqkv"][QD + KD:])),
+                (b + "attn_q_norm.weight", vec(L["q_norm"])),
+                (b + "attn_k_norm.weight", vec(L["k_norm"])),
+                (b + "attn_output.weight", mat(L["wo"])),
+                (b + "ffn_norm.weight", vec(L["ffn_norm"])),
+                (b + "ffn_gate.weight", mat(L["wg"])),
+                (b + "ffn_up.weight", mat(L["wu"])),
+                (b + "ffn_down.weight", mat(L["wd"]))]
+    return out
+
+
+def qwen3_metadata(model, n_ctx: int = 4096, alignment: int = 32) -> list[tuple[str, int, object]]:
+    return [("general.architecture", T_STRING, "qwen3"),
+            ("general.name", T_STRING, "tiny synthetic qwen3"),
+            ("general.alignment", T_U32, alignment),
+            ("qwen3.block_count", T_U32, model.n_layer),
+            ("qwen3.context_length", T_U32, n_ctx),
+            ("qwen3.embedding_length", T_U32, model.E),
+            ("qwen3.feed_forward_length", T_U32, model.layers[0]["wg"].shape[0]),
+            ("qwen3.attention.head_count", T_U32, model.H),
+            ("qwen3.attention.head_count_kv", T_U32, model.HKV),
+            ("qwen3.attention.key_length", T_U32, 128),
+            ("qwen3.attention.value_length", T_U32, 128),
+            ("qwen3.rope.dimension_count", T_U32, 128),
+            ("qwen3.rope.freq_base", T_F32, 1e6),
+            ("qwen3.attention.layer_norm_rms_epsilon", T_F32, 1e-6)]
+
+
+def write_gguf(path, metadata, tensors, alignment: int = 32, version: int = 3) -> None:
+    """metadata: (key, type id, value); tensors: (name, array) with ne = array.shape[::-1]."""
+    head = struct.pack("<IIQQ", 0x46554747, version, len(tensors), len(metadata))
+    head += b"".join(_kv(k, t, v) for k, t, v in metadata)
+    offsets, off = [], 0
+    for _, a in tensors:
+        offsets.append(off)
+        off += (a.nbytes + alignment - 1) // alignment * alignment
+    for (name, a), o in zip(tensors, offsets):
+        ty = 1 if a.dtype == np.float16 else 0
+        head += _s(name) + struct.pack("<I", a.ndim) + b"".join(struct.pack("<Q", n) for n in a.shape[::-1])
+        head += struct.pack("<IQ", ty, o)
+    pad = (-len(head)) % alignment
+    with open(path, "wb") as f:
+        f.write(head + b"\0" * pad)
+        for (_, a), o in zip(tensors, offsets):
+            b = a.tobytes()
+            f.write(b + b"\0" * ((-len(b)) % alignment))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("out")
+    ap.add_argument("--f16", action="store_true")
+    ap.add_argument("--seed", type=int, default=7)
+    a = ap.parse_args()
+    from tests.tiny_qwen3 import TinyQwen3
+    model = TinyQwen3(seed=a.seed)
+    write_gguf(a.out, qwen3_metadata(model), qwen3_tensors(model, a.f16))
+    print("wrote", a.out)
+
+
+if __name__ == "__main__":
+    main()

@@ -131,3 +131,24 @@ def test_serve_prefix_reuse_equals_generate(orc, gpu):
         assert d <= LOGPROB_TOL, f"{name}: |d logprob| {d:.2e}"
     starts = {name: s for name, _, _, s in cases}
     assert starts["continuation"] == len(p1) + 5 and starts["same prompt"] == len(p1) - 1 and starts["unrelated"] == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("f16", [False, True])
+def test_e2e_logprob_model_read_from_gguf(orc, gpu, tmp_path, f16):
+    """The gate on a model that reaches the harness through a GGUF file and this build's reader
+    (tests/golden/write_tiny_gguf.py writes it; read_config / read_tensors validation,
+    src/model.cpp:38-103): F32 and F16 weights, HIP attention against the reference's."""
+    import torch
+    from tests.golden.write_tiny_gguf import qwen3_metadata, qwen3_tensors, write_gguf
+    src = TinyQwen3(seed=41, n_layer=3, n_head=8, n_head_kv=2)
+    path = tmp_path / "tiny.gguf"
+    write_gguf(path, qwen3_metadata(src), qwen3_tensors(src, f16))
+    model = TinyQwen3.from_gguf(path)
+    toks = np.random.default_rng(42).integers(0, model.V, size=sum(CHUNKS) + N_DECODE + 1)
+    ref = run_sequence(model, oracle_attention(model, orc), toks, CHUNKS, N_DECODE, N_CTX)
+    hip = run_sequence(model, _hip_attention(model, gpu, torch), toks, CHUNKS, N_DECODE, N_CTX)
+    d = float(np.max(np.abs(hip - ref)))
+    print(f"e2e from GGUF ({'F16' if f16 else 'F32'}): max |d logprob| = {d:.3e} over {len(ref)} positions",
+          flush=True)
+    assert d <= LOGPROB_TOL, f"max |delta logprob| {d:.2e} > {LOGPROB_TOL}"

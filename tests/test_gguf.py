@@ -1,0 +1,201 @@
+"""The GGUF reader (exactinfer_amd/host/gguf.cpp through include/ei_gguf.h), CPU only.
+
+Files come from tests/golden/write_tiny_gguf.py (a tiny synthetic Qwen3; no real Qwen3 GGUF
+exists here, so a real file stays unread).  Checked: the tensor table and metadata against the
+writer's inputs and against an independent minimal parser; Qwen3 configuration and shape
+validation (read_config / read_tensors, src/model.cpp:38-103); and every class of malformed file
+the reference reader rejects (src/gguf.cpp:203-254): truncation anywhere, wrong magic or version,
+implausible counts, bad dimensions or types, repeated keys or names, bad alignment, tensors
+misaligned or past the end.  The forward pass of the model read back equals the in-memory one."""
+import struct
+
+import numpy as np
+import pytest
+
+from tests.golden.write_tiny_gguf import T_STRING, T_U32, qwen3_metadata, qwen3_tensors, write_gguf
+from tests.tiny_qwen3 import TinyQwen3, oracle_attention, run_sequence
+
+
+@pytest.fixture(scope="module")
+def model():
+    return TinyQwen3(seed=7)
+
+
+def _write(tmp_path, model, f16=False, name="m.gguf", meta=None, tensors=None, **kw):
+    p = tmp_path / name
+    write_gguf(p, meta if meta is not None else qwen3_metadata(model),
+               tensors if tensors is not None else qwen3_tensors(model, f16), **kw)
+    return p
+
+
+def _parse_independently(path):
+    """A minimal parser of the tensor table (a second reading of the format, not the reader)."""
+    b = path.read_bytes()
+    at = [0]
+
+    def rd(fmt):
+        v = struct.unpack_from(fmt, b, at[0])
+        at[0] += struct.calcsize(fmt)
+        return v[0]
+
+    def rs():
+        n = rd("<Q")
+        s = b[at[0]:at[0] + n].decode()
+        at[0] += n
+        return s
+
+    assert rd("<I") == 0x46554747
+    rd("<I")
+    nt, nkv = rd("<Q"), rd("<Q")
+    meta = {}
+    for _ in range(nkv):
+        k, t = rs(), rd("<I")
+        meta[k] = rs() if t == T_STRING else rd({4: "<I", 6: "<f", 5: "<i", 10: "<Q", 12: "<d"}[t])
+    tensors = {}
+    for _ in range(nt):
+        name, nd = rs(), rd("<I")
+        ne = [rd("<Q") for _ in range(nd)]
+        tensors[name] = (ne, rd("<I"), rd("<Q"))
+    align = meta.get("general.alignment", 32)
+    return meta, tensors, (at[0] + align - 1) // align * align
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_reader_returns_what_was_written(tmp_path, model, f16):
+    from exactinfer_amd.gguf import GgufFile
+    p = _write(tmp_path, model, f16)
+    tens = qwen3_tensors(model, f16)
+    meta_i, tab_i, data_start = _parse_independently(p)
+    raw = p.read_bytes()
+    with GgufFile(p) as g:
+        assert g.version == 3
+        assert g.tensor_names() == [n for n, _ in tens]
+        for name, a in tens:
+            got = g.tensor(name)
+            assert got.dtype == a.dtype and got.shape == a.shape, name
+            assert np.array_equal(got.view(np.uint8), a.view(np.uint8)), name
+            ty, ne, nb = g.tensor_info(name)
+            assert (ne, ty) == (tab_i[name][0], tab_i[name][1]) and nb == a.nbytes
+            off = data_start + tab_i[name][2]
+            assert raw[off:off + nb] == a.tobytes()
+        assert g.get_str("general.architecture") == "qwen3"
+        assert g.get_int("qwen3.block_count") == model.n_layer == meta_i["qwen3.block_count"]
+        assert g.get_float("qwen3.rope.freq_base") == np.float32(1e6)
+        assert g.get_float("qwen3.block_count") == model.n_layer  # integers read as numbers too
+        c = g.qwen3_config()
+        assert (c["n_layer"], c["n_embd"], c["n_head"], c["n_head_kv"], c["head_dim"], c["rope_dim"], c["n_vocab"],
+                c["n_ff"], c["n_ctx_train"]) == (model.n_layer, model.E, model.H, model.HKV, 128, 128, model.V, 512,
+                                                 4096)
+        assert np.float32(c["eps"]) == np.float32(1e-6) and c["rope_base"] == np.float32(1e6)
+        assert g.tensor_info("no.such.tensor") is None
+
+
+def test_missing_and_mistyped_metadata(tmp_path, model):
+    from exactinfer_amd.gguf import GgufError, GgufFile
+    with GgufFile(_write(tmp_path, model)) as g:
+        with pytest.raises(GgufError, match="metadata missing"):
+            g.get_int("qwen3.nothing")
+        with pytest.raises(GgufError, match="not an integer"):
+            g.get_int("general.architecture")
+        with pytest.raises(GgufError, match="not a string"):
+            g.get_str("qwen3.block_count")
+        with pytest.raises(GgufError, match="tensor missing"):
+            g.tensor("nothing")
+
+
+def test_model_read_back_runs_the_same_forward(tmp_path, model, orc):
+    """The model loaded through the reader gives bit-identical logprobs to the one written."""
+    toks = np.random.default_rng(8).integers(0, model.V, 41)
+    ref = run_sequence(model, oracle_attention(model, orc), toks, [16, 16], 8, 64)
+    m2 = TinyQwen3.from_gguf(_write(tmp_path, model))
+    got = run_sequence(m2, oracle_attention(m2, orc), toks, [16, 16], 8, 64)
+    assert np.array_equal(got, ref)
+    m16 = TinyQwen3.from_gguf(_write(tmp_path, model, f16=True, name="h.gguf"))
+    assert np.array_equal(m16.layers[1]["wo"], model.layers[1]["wo"].astype(np.float16).astype(np.float32))
+
+
+def _expect_rejected(path, match):
+    from exactinfer_amd.gguf import GgufError, GgufFile
+    with pytest.raises(GgufError, match=match):
+        GgufFile(path)
+
+
+def test_truncated_files_are_rejected_anywhere(tmp_path, model):
+    p = _write(tmp_path, model)
+    raw = p.read_bytes()
+    meta_i, tab_i, data_start = _parse_independently(p)
+    last = max(tab_i.values(), key=lambda t: t[2])
+    cuts = [0, 3, 7, 20, 40, 100, 300, data_start - 1, data_start + last[2] + 5]
+    for k, cut in enumerate(cuts):
+        q = tmp_path / f"cut{k}.gguf"
+        q.write_bytes(raw[:cut])
+        _expect_rejected(q, "empty|ends early|past the end|wrong magic")
+
+
+def _patched(tmp_path, raw, off, fmt, value, name):
+    b = bytearray(raw)
+    struct.pack_into(fmt, b, off, value)
+    q = tmp_path / name
+    q.write_bytes(bytes(b))
+    return q
+
+
+def test_header_errors(tmp_path, model):
+    raw = _write(tmp_path, model).read_bytes()
+    _expect_rejected(_patched(tmp_path, raw, 0, "<I", 0x46554748, "magic.gguf"), "wrong magic")
+    _expect_rejected(_patched(tmp_path, raw, 4, "<I", 1, "v1.gguf"), "version 1")
+    _expect_rejected(_patched(tmp_path, raw, 8, "<Q", 200000, "nt.gguf"), "count is not plausible")
+    _expect_rejected(_patched(tmp_path, raw, 16, "<Q", 1 << 40, "nkv.gguf"), "count is not plausible")
+    # the first key's string length
+    _expect_rejected(_patched(tmp_path, raw, 24, "<Q", 1 << 30, "slen.gguf"), "string length")
+
+
+def test_tensor_table_errors(tmp_path, model):
+    from tests.golden.write_tiny_gguf import _s
+    tens = qwen3_tensors(model, False)
+    meta = qwen3_metadata(model)
+    # repeated key / tensor name
+    _expect_rejected(_write(tmp_path, model, name="k.gguf", meta=meta + [meta[1]]), "key repeated")
+    _expect_rejected(_write(tmp_path, model, name="t.gguf", tensors=tens + [tens[0]]), "name repeated")
+    # bad alignment value
+    bad = [m if m[0] != "general.alignment" else (m[0], T_U32, 48) for m in meta]
+    _expect_rejected(_write(tmp_path, model, name="a.gguf", meta=bad, alignment=32), "alignment 48")
+    # patch the first tensor's info: n_dims 0, unknown type, misaligned and out-of-range offsets
+    p = _write(tmp_path, model, name="base.gguf")
+    raw = p.read_bytes()
+    i = raw.index(_s("token_embd.weight")) + len(_s("token_embd.weight"))
+    _expect_rejected(_patched(tmp_path, raw, i, "<I", 0, "nd.gguf"), "0 dimensions")
+    _expect_rejected(_patched(tmp_path, raw, i, "<I", 5, "nd5.gguf"), "5 dimensions")
+    _expect_rejected(_patched(tmp_path, raw, i + 4, "<Q", 0, "dim0.gguf"), "bad shape")
+    _expect_rejected(_patched(tmp_path, raw, i + 20, "<I", 99, "ty.gguf"), "unknown type 99")
+    q8 = _patched(tmp_path, raw, i + 20, "<I", 8, "q8.gguf").read_bytes()  # Q8_0: blocks of 32 elements
+    _expect_rejected(_patched(tmp_path, q8, i + 4, "<Q", 48, "blk.gguf"), "whole number of blocks")
+    _expect_rejected(_patched(tmp_path, raw, i + 24, "<Q", 4, "mis.gguf"), "not aligned")
+    _expect_rejected(_patched(tmp_path, raw, i + 24, "<Q", 1 << 32, "far.gguf"), "past the end")
+
+
+def test_qwen3_validation(tmp_path, model):
+    from exactinfer_amd.gguf import GgufError, GgufFile
+    meta = qwen3_metadata(model)
+    tens = qwen3_tensors(model, False)
+
+    def cfg_error(meta_=None, tens_=None, name="x.gguf"):
+        with GgufFile(_write(tmp_path, model, name=name, meta=meta_ or meta, tensors=tens_ or tens)) as g:
+            with pytest.raises(GgufError) as e:
+                g.qwen3_config()
+        return str(e.value)
+
+    arch = [m if m[0] != "general.architecture" else (m[0], T_STRING, "llama") for m in meta]
+    assert "unsupported architecture" in cfg_error(arch, name="arch.gguf")
+    assert "RoPE scaling" in cfg_error(meta + [("qwen3.rope.scaling.type", T_STRING, "linear")], name="rs.gguf")
+    odd = [m if m[0] != "qwen3.attention.head_count_kv" else (m[0], T_U32, 3) for m in meta]
+    assert "invalid model configuration" in cfg_error(odd, name="kv.gguf")
+    no_norm = [t for t in tens if t[0] != "blk.1.attn_k_norm.weight"]
+    assert "tensor missing: blk.1.attn_k_norm.weight" in cfg_error(tens_=no_norm, name="nn.gguf")
+    bias = tens + [("blk.0.attn_q.bias", np.zeros(512, np.float32))]
+    assert "bias" in cfg_error(tens_=bias, name="bias.gguf")
+    wrong = [(n, a if n != "blk.0.attn_v.weight" else a[:128]) for n, a in tens]
+    assert "blk.0.attn_v.weight has shape [256,128], expected [256,256]" in cfg_error(tens_=wrong, name="sh.gguf")
+    # a tied embedding (no output.weight) is accepted
+    with GgufFile(_write(tmp_path, model, name="tied.gguf", tensors=[t for t in tens if t[0] != "output.weight"])) as g:
+        assert g.qwen3_config()["n_vocab"] == model.V

@@ -60,6 +60,35 @@ class TinyQwen3:
         self.out_norm = norm_w(n_embd)
         self.lm = mat(n_vocab, n_embd, gain=2.0)
 
+    @classmethod
+    def from_gguf(cls, path) -> "TinyQwen3":
+        """The model a GGUF file holds, read through this build's C++ reader (exactinfer_amd.gguf):
+        configuration and tensor table validated as read_config / read_tensors do
+        (src/model.cpp:38-103); F16 matrices widened to float32 exactly."""
+        from exactinfer_amd.gguf import GgufFile
+        self = cls.__new__(cls)
+        D = HEAD_DIM
+        with GgufFile(path) as g:
+            c = g.qwen3_config()
+            if c["head_dim"] != D or c["rope_dim"] != D:
+                raise ValueError("the harness is built for head_dim = rope_dim = 128")
+            t = lambda n: np.ascontiguousarray(g.tensor(n), dtype=np.float32)
+            self.n_layer, self.E, self.H, self.HKV, self.V = (c["n_layer"], c["n_embd"], c["n_head"], c["n_head_kv"],
+                                                              c["n_vocab"])
+            self.emb = t("token_embd.weight")
+            self.out_norm = t("output_norm.weight")
+            self.lm = t("output.weight") if g.tensor_info("output.weight") else self.emb
+            self.layers = []
+            for l in range(self.n_layer):
+                b = f"blk.{l}."
+                self.layers.append(dict(
+                    attn_norm=t(b + "attn_norm.weight"),
+                    wqkv=np.concatenate([t(b + "attn_q.weight"), t(b + "attn_k.weight"), t(b + "attn_v.weight")]),
+                    q_norm=t(b + "attn_q_norm.weight"), k_norm=t(b + "attn_k_norm.weight"),
+                    wo=t(b + "attn_output.weight"), ffn_norm=t(b + "ffn_norm.weight"),
+                    wg=t(b + "ffn_gate.weight"), wu=t(b + "ffn_up.weight"), wd=t(b + "ffn_down.weight")))
+        return self
+
     @property
     def qkv_width(self) -> int:
         return (self.H + 2 * self.HKV) * HEAD_DIM
