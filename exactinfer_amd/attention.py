@@ -117,10 +117,11 @@ class DecodeWorkspace:
         _capi.call("ei_attn_workspace_init", _stream(), self.buf.data_ptr(), self.nbytes)
 
     def status(self) -> int:
-        """The workspace's sticky status word (uint32 at nbytes - 256; bit 0: the splits of one
+        """The workspace's sticky status word (uint32 at (nbytes - 256) & ~255; bit 0: the splits of one
         (sequence, KV head) ran on different XCDs, against the placement the in-kernel split
         merge relies on).  Synchronises the stream."""
-        word = self.buf[self.nbytes - 256:self.nbytes - 252].cpu()
+        at = (self.nbytes - 256) & ~255
+        word = self.buf[at:at + 4].cpu()
         return int(word.view(torch.int32)[0]) & 0xFFFFFFFF
 
 
@@ -202,8 +203,8 @@ def decode_step_paged(qkv: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, blo
 
 # ---------------------------------------------------------------- prefill
 class PrefillWorkspace:
-    """Key-split shares for ei_attn_prefill_split: serves chunks of up to max_B rows with
-    pos0 + B <= max_kv (max_kv only steers the split plan; larger positions stay correct)."""
+    """Key-split shares for ei_attn_prefill_split / ei_prefill_step: serves chunks of up to max_B
+    rows with pos0 + B <= max_kv (max_kv only steers the split plan; larger positions stay correct)."""
 
     def __init__(self, max_B: int, n_head: int, n_head_kv: int, max_kv: int, device="cuda"):
         self.max_B, self.max_kv = max_B, max_kv

@@ -153,14 +153,18 @@ int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void
                   bool launch_combine = false) {
     REQUIRE(max_kv > 0, "max_kv %d must be positive", max_kv);
     REQUIRE(ws != nullptr && aligned16(ws), "workspace missing or not 16-byte aligned");
-    const size_t need = ei::decode_ws_bytes(n_seq, a.H, a.HKV, max_kv);
-    REQUIRE(ws_bytes >= need, "workspace of %zu bytes < %zu needed (ei_attn_decode_ws_bytes)", ws_bytes, need);
     const ei::DecodePlan p = ei::decode_plan(n_seq, a.HKV, max_kv, a.block_table != nullptr);
     const ei::DecodeWsLayout lay = ei::decode_ws_layout(n_seq, a.H, a.HKV, max_kv);
+    REQUIRE(ei::ws_fits(ws_bytes, lay.partials, lay.units),
+            "workspace of %zu bytes too small for n_seq %d, max_kv %d (ei_attn_decode_ws_bytes gives %zu)", ws_bytes,
+            n_seq, max_kv, ei::decode_ws_bytes(n_seq, a.H, a.HKV, max_kv));
     char* base = static_cast<char*>(ws);
     a.part_acc = reinterpret_cast<float*>(base);  // partials are laid out with the kernel's head slots
     a.rec = reinterpret_cast<uint32_t*>(base + lay.rec);
-    a.status = reinterpret_cast<uint32_t*>(base + lay.status);
+    // the status word and the arrival counters below it sit where the workspace's size puts them,
+    // so every call on it finds them at the same addresses whatever its plan
+    a.status = reinterpret_cast<uint32_t*>(base + ei::ws_status_offset(ws_bytes));
+    a.ctr_top = a.status;
     a.chunk = p.chunk;
     a.nsplit = p.nsplit;
     a.units = n_seq * a.HKV;
@@ -249,8 +253,9 @@ int decode_step_impl(ei_stream_t stream, const float* qkv, long row_stride, floa
     a.eps = eps;
     if (no_alloc) {
         REQUIRE(max_kv > 0, "max_kv %d must be positive", max_kv);
+        const ei::DecodeWsLayout lay = ei::decode_ws_layout(n_seq, n_head, n_head_kv, max_kv);
         const size_t need = ei::decode_ws_bytes(n_seq, n_head, n_head_kv, max_kv);
-        REQUIRE(need <= ei::kDecodeScratchBytes,
+        REQUIRE(ei::ws_fits(ei::kDecodeScratchBytes, lay.partials, lay.units),
                 "n_seq %d, n_head %d, n_head_kv %d, max_kv %d need %zu bytes of scratch; the allocation-free step has "
                 "%zu (use ei_decode_step with a workspace)",
                 n_seq, n_head, n_head_kv, max_kv, need, ei::kDecodeScratchBytes);

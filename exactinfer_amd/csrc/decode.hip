@@ -59,6 +59,7 @@ constexpr int kTile = 16;                          // keys per wave tile
 constexpr int kTileFloats = 2 * kTile * kHeadDim;  // K rows then V rows
 constexpr int kRingTiles = 8;                      // LDS ring: 8 tiles (128 KB) per workgroup
 constexpr int kRec = 32;                           // uint32s per split record: one 128-byte line
+constexpr int kCtrStride = 64;                     // uint32s between arrival counters (256 bytes)
 
 // Transposing butterfly over the 8 lanes c = lane%8 (masks 1, 2, 4).  At each step a
 // lane keeps one half of its array and receives the partner's copy of that half, so N
@@ -308,12 +309,9 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane >> 3, c = lane & 7;
-    // in-kernel merge: this split's flag and this launch's epoch (read now, used at the end)
-    // (the record line is also brought into the L2 here, long before it is written and read)
+    // this split's record line (its (m, l) per head slot; word 1: the XCD it ran on)
     uint32_t* unit_rec = a.rec + (size_t)unit * S * kRec;
     uint32_t* my_rec = unit_rec + split * kRec;
-    uint32_t epoch = 0;
-    if (S > 1 && tid == 0) epoch = *my_rec + 1u;
     const int len = a.kv_len ? a.kv_len[seq] : (*a.pos_dev + 1);
     const size_t KD = (size_t)a.HKV * D;
     const size_t row0 = a.kv_offset ? (size_t)a.kv_offset[seq] : 0;
@@ -601,8 +599,8 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
         return;
     }
 
-    // unnormalised partial of this split: acc rows, then the split's record line (epoch, and
-    // (m, l) of each head slot), written whole by one instruction so the line is valid in the L2
+    // unnormalised partial of this split: acc rows, then the split's record line (written whole
+    // by one instruction, so the line is valid in the L2 without a fill)
     if (tid < NCOL && gcol < Gr) *reinterpret_cast<float4*>(a.part_acc + (slot * G + gcol) * D + 4 * d4) = o;
     __shared__ float mlsh[2 * G];
     __shared__ int is_last;
@@ -614,37 +612,39 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     if (merging) wait_vmcnt<0>();  // this thread's acc stores are in the L2 before the record is
     __syncthreads();
     if (w == 0) {
-        const uint32_t e = __builtin_amdgcn_readfirstlane(epoch);
-        uint32_t xcc = 0;  // the XCD this workgroup runs on (record word 1)
+        uint32_t xcc = 0;
         if (merging) asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
         if (lane < kRec)
-            my_rec[lane] = lane == 0 ? e : lane == 1 ? xcc : lane >= 2 && lane < 2 + 2 * G ? __float_as_uint(mlsh[lane - 2]) : 0u;
+            my_rec[lane] = lane == 1 ? xcc : lane >= 2 && lane < 2 + 2 * G ? __float_as_uint(mlsh[lane - 2]) : 0u;
         if (merging) {
             // In-kernel merge.  Every split of the unit ran on this XCD, so the partials meet in
             // its L2: a store is acknowledged by the L2 (vmcnt), and loads that miss the CU's L1
-            // read it there.  Each workgroup publishes its record with this launch's epoch (the
-            // record's previous value + 1) and reads the epochs of all the unit's records; one
-            // that finds every record at its epoch merges.  The workgroup whose record reached
-            // the L2 last always finds them all, since the others' were acknowledged before it;
-            // if several find them all, each writes the same bits.  No atomics (they serialise
-            // on one address) and no L2 write-back or invalidate (a device-wide fence costs more
+            // read it there.  Once its partial and record are acknowledged, a workgroup counts
+            // itself in on the unit's arrival counter (a line of its own); the one that brings
+            // it to S merges and sets it back to zero for the next launch, whatever that
+            // launch's plan.  No L2 write-back or invalidate (a device-wide fence costs more
             // than the whole decode on this part).
-            wait_vmcnt<0>();  // the record is in the L2 before the others are read
-            bool all = true, same_xcd = true;
-            for (int s0 = 0; s0 < S; s0 += 64) {
-                const int sx = s0 + lane;
-                uint32_t f = e, fx = xcc;
-                if (sx < S) {
-                    f = __hip_atomic_load(unit_rec + sx * kRec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    fx = __hip_atomic_load(unit_rec + sx * kRec + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                }
-                all = all && __builtin_amdgcn_ballot_w64(f != e) == 0;
-                same_xcd = same_xcd && __builtin_amdgcn_ballot_w64(fx != xcc) == 0;
+            wait_vmcnt<0>();  // the record is in the L2 before the count
+            uint32_t old = 0;
+            if (lane == 0) {
+                uint32_t* ctr = a.ctr_top - (size_t)(unit + 1) * kCtrStride;
+                old = atomicAdd(ctr, 1u);
+                if (old == (uint32_t)S - 1) atomicSub(ctr, (uint32_t)S);
             }
-            // the placement the protocol relies on (workgroups b and b + n_xcc share an XCD; the
-            // dispatcher's starting XCD may rotate between launches) held for every split
-            if (lane == 0 && all && !same_xcd) atomicOr(a.status, 1u);
-            if (lane == 0) is_last = all;
+            const bool last = __builtin_amdgcn_readfirstlane(old) == (uint32_t)S - 1;
+            if (last) {  // the placement the protocol relies on (workgroups b and b + n_xcc share an
+                         // XCD; the dispatcher's starting XCD may rotate between launches) held
+                bool same_xcd = true;
+                for (int s0 = 0; s0 < S; s0 += 64) {
+                    const int sx = s0 + lane;
+                    const uint32_t fx = sx < S ? __hip_atomic_load(unit_rec + sx * kRec + 1, __ATOMIC_RELAXED,
+                                                                   __HIP_MEMORY_SCOPE_WORKGROUP)
+                                               : xcc;
+                    same_xcd = same_xcd && __builtin_amdgcn_ballot_w64(fx != xcc) == 0;
+                }
+                if (lane == 0 && !same_xcd) atomicOr(a.status, 1u);
+            }
+            if (lane == 0) is_last = last;
         }
     }
     if (!merging) return;  // k_combine merges the splits in a second launch
@@ -754,12 +754,15 @@ DecodeWsLayout decode_ws_layout(int n_seq, int H, int HKV, int max_kv) {
     const int G = decode_group_slots(H / HKV);
     DecodeWsLayout l;
     l.rec = align256(slots * G * kHeadDim * 4);
-    l.status = l.rec + align256(slots * kRec * 4);
-    l.total = l.status + 256;
+    l.partials = l.rec + align256(slots * kRec * 4);
+    l.units = (size_t)n_seq * HKV;
     return l;
 }
 
-size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv) { return decode_ws_layout(n_seq, H, HKV, max_kv).total; }
+size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv) {
+    const DecodeWsLayout l = decode_ws_layout(n_seq, H, HKV, max_kv);
+    return ws_bytes_for(l.partials, l.units);
+}
 
 template <int G, int NW>
 static hipError_t launch_gw(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused) {

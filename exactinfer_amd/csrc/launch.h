@@ -9,6 +9,26 @@
 
 namespace ei {
 
+// Workspaces of the decode's split merge are laid out by their size alone, so that
+// calls of any plan on one workspace agree: the status word at the top, below it a zone of
+// arrival counters (one 256-byte line per unit, unit u at (u + 1) lines below the status word;
+// every call leaves them at zero), and the partials of the call's plan from the start.  The
+// counter zone is the top sixteenth, so partials and counters never overlap whatever the plan.
+inline size_t ws_status_offset(size_t ws_bytes) { return (ws_bytes - 256) & ~(size_t)255; }
+inline size_t ws_counter_zone(size_t ws_bytes) { return (ws_bytes / 16) & ~(size_t)255; }
+// workspace bytes for partials of up to `partials` bytes and up to `units` counters
+inline size_t ws_bytes_for(size_t partials, size_t units) {
+    const size_t a = ((partials + 1024) * 16 / 15 + 255) & ~(size_t)255;
+    const size_t b = (units * 256 * 16 + 1024 + 255) & ~(size_t)255;
+    return a > b ? a : b;
+}
+// whether a call's partials and counters fit the workspace's zones
+inline bool ws_fits(size_t ws_bytes, size_t partials, size_t units) {
+    if (ws_bytes < 1024) return false;
+    const size_t zone = ws_counter_zone(ws_bytes);
+    return units * 256 <= zone && partials + zone + 512 <= ws_bytes;
+}
+
 // Opt kernel f into `bytes` of dynamic LDS (> 64 KB needs it) once per process.  Setting the
 // attribute is idempotent, so first launches racing from several host threads only repeat it.
 inline hipError_t opt_in_lds(std::atomic<bool>& done, const void* f, size_t bytes) {
@@ -41,10 +61,9 @@ constexpr int kDecodeMaxSplits = 256;
 constexpr int kDecodePagedMaxChunk = 8192;  // 4 waves x 128 tiles of 16 keys
 DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged);
 size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv);
-// byte offsets of the workspace parts: partial accumulators at 0, then the split records and
-// the status word (the last 256 bytes)
+// the call's partials: accumulators at 0, then the split records (ending at `partials`)
 struct DecodeWsLayout {
-    size_t rec, status, total;
+    size_t rec, partials, units;
 };
 DecodeWsLayout decode_ws_layout(int n_seq, int H, int HKV, int max_kv);
 int decode_group_slots(int g);  // heads per KV head the decode kernel is built for (0: unsupported)
@@ -65,8 +84,11 @@ struct DecodeArgs {
     float scale;
     int chunk, nsplit;
     float* part_acc;        // [n_seq*HKV*nsplit][G][128]
-    uint32_t* rec;          // [n_seq*HKV*nsplit][32]: split record line, word 0 the merge epoch,
+    uint32_t* rec;          // [n_seq*HKV*nsplit][32]: split record line, word 1 the XCD it ran on,
                             // words 2+2g, 3+2g the (m, l) of head slot g (float bits)
+    uint32_t* ctr_top;      // the workspace's status word; unit u's arrival counter of the in-kernel
+                            // merge sits (u+1)*256 bytes below it, wherever the call's plan puts its
+                            // partials (zero between launches)
     uint32_t* status;       // sticky word: bit 0 set when a workgroup ran on another XCD than its grid slot says
     int units;              // n_seq * HKV
     int n_xcc;              // XCDs the grid is spread over (workgroup b runs on XCD b % n_xcc)

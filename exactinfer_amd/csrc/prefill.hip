@@ -59,6 +59,8 @@
 // and then unit nu-1-p; every workgroup has the same amount of work.  Workgroup id
 // L -> kv head L % HKV first, so with 8 KV heads all blocks of one KV head share an
 // XCD (and its L2) under the round-robin XCD dispatch.
+#include <cstdlib>
+
 #include "common.h"
 #include "launch.h"
 
@@ -563,6 +565,10 @@ int prefill_split(int B, int H, int HKV, int max_kv) {
     int best = 1;
     for (int k = 2; k <= kmax; ++k)
         if (rounds(k) < 0.9 * rounds(best)) best = k;
+    if (const char* env = std::getenv("EI_PREFILL_SPLIT")) {  // tuning override (1..8)
+        const int v = std::atoi(env);
+        if (v >= 1 && v <= kPrefillMaxSplit) best = v;
+    }
     return best;
 }
 

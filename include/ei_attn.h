@@ -98,16 +98,18 @@ int ei_qkv_prepare(ei_stream_t stream, float* qkv, int rows, long row_stride, in
 
 /* ------------------------------------------------------------------ decode (split-K)
  * Workspace for the decode entry points: per (sequence, kv head, key split) partial
- * (m, l, acc), one arrival counter per (sequence, kv head) for the in-kernel split merge,
- * and a status word in its last 256 bytes.  max_kv sizes the split grid (fixed, so a
- * captured graph stays valid as positions advance); a sequence longer than max_kv is still
- * attended in full (its last split takes the excess keys), only more slowly.
- * The workspace must be zero-filled once before its first use, by ei_attn_workspace_init
- * (a fill kernel, not a memset, so it may be captured) or any other zero fill; every decode
- * call leaves the counters at zero again.  Status word (uint32 at ws + ws_bytes - 256, as
- * sized by ei_attn_decode_ws_bytes): bit 0 is set, and stays set, if the splits of one
- * (sequence, kv head) were ever found on different XCDs, against the round-robin placement
- * the in-kernel merge relies on (never seen on MI355X; that merge is then unreliable: set
+ * (m, l, acc), one arrival counter per (sequence, kv head) for the in-kernel split merge, and a
+ * status word.  Its layout follows from its size alone, so calls of different plans (n_seq,
+ * max_kv, paged or not) may share it one after another: partials from the start, the counters in
+ * the top sixteenth, the status word (uint32) at ws + ((ws_bytes - 256) & ~255), ws_bytes as passed
+ * to the calls.  A call whose plan does not fit is rejected (EI_ERR_ARG).  max_kv sizes the split
+ * grid (fixed, so a captured graph stays valid as positions advance); a sequence longer than
+ * max_kv is still attended in full (its last split takes the excess keys), only more slowly.
+ * The workspace must be zero-filled once before its first use, by ei_attn_workspace_init (a
+ * fill kernel, not a memset, so it may be captured) or any other zero fill; every decode call
+ * leaves the counters at zero again.  Status bit 0 is set, and stays set, if the splits of one
+ * (sequence, kv head) were ever found on different XCDs, against the round-robin placement the
+ * in-kernel merge relies on (never seen on MI355X; that merge is then unreliable: set
  * EI_DECODE_MERGE=launch for the two-launch combine).  Calls that share a workspace must not
  * overlap in time. */
 size_t ei_attn_decode_ws_bytes(int n_seq, int n_head, int n_head_kv, int max_kv);

@@ -255,3 +255,59 @@ def test_fused_decode_partial_rope_dim(orc, gpu, paged):
                               v[idx].reshape(n, HKV, D), n, H, HKV, D)
         assert rel_err(out[s], ref) <= ATTN_RTOL, f"sequence {s}"
     assert bits_equal(_host(kc), k) and bits_equal(_host(vc), v)
+
+
+def test_one_workspace_serves_calls_of_different_plans(orc, gpu):
+    """Decode calls of different plans (n_seq, max_kv, contiguous or paged) take turns on one
+    workspace, several with the in-kernel split merge: its arrival counters sit where the
+    workspace's size puts them, so every call finds them at zero whatever the previous plan wrote."""
+    import torch
+    from exactinfer_amd import _capi
+    H, HKV = 32, 8
+    shape = gpu.AttnShape(H, HKV)
+    ws = gpu.DecodeWorkspace(4, H, HKV, max_kv=16384)
+    rows = 40000
+    k, v = orc.normal((rows, HKV * D), 3800), orc.normal((rows, HKV * D), 3801)
+    kd, vd = _dev(k), _dev(v)
+    scale = gpu.default_scale()
+    calls = [("contiguous", [16000], 16384), ("contiguous", [9000, 3000, 16384, 500], 16384),
+             ("paged", [12000, 7000], 12288), ("contiguous", [5000], 5000), ("contiguous", [16000], 16384),
+             ("paged", [2000, 4000, 9000], 16384), ("contiguous", [300, 8000, 15000, 2], 16000)]
+    for i, (kind, lens, max_kv) in enumerate(calls):
+        lens = np.array(lens, np.int32)
+        n = len(lens)
+        q = orc.normal((n, H * D), 3900 + i)
+        out = torch.full((n, H, D), float("nan"), device="cuda")
+        # (device copies held in names: a temporary's memory could be reused before the launch reads it)
+        qd, ld = _dev(q), _dev(lens)
+        if kind == "contiguous":
+            offs = np.array([(s * 9001) % (rows - int(lens[s])) for s in range(n)], np.int64)
+            od = _dev(offs)
+            _capi.call("ei_attn_decode_batched", gpu._stream(), qd.data_ptr(), H * D, out.data_ptr(), kd.data_ptr(),
+                       vd.data_ptr(), od.data_ptr(), ld.data_ptr(), n, H, HKV, D, float(scale), max_kv,
+                       ws.buf.data_ptr(), ws.nbytes)
+            row_of = lambda s, t: int(offs[s]) + t
+        else:
+            bs = 64
+            nblk = [-(-int(x) // bs) for x in lens]
+            table = np.zeros((n, max(max(nblk), -(-max_kv // bs))), np.int32)  # covers max_kv
+            perm = np.random.default_rng(3950 + i).permutation(rows // bs)
+            k0 = 0
+            for s_, nb in enumerate(nblk):
+                table[s_, :nb] = perm[k0:k0 + nb]
+                k0 += nb
+            td = _dev(table)
+            _capi.call("ei_attn_decode_paged", gpu._stream(), qd.data_ptr(), H * D, out.data_ptr(), kd.data_ptr(),
+                       vd.data_ptr(), td.data_ptr(), table.shape[1], bs, ld.data_ptr(), n, H, HKV, D,
+                       float(scale), max_kv, ws.buf.data_ptr(), ws.nbytes)
+            row_of = lambda s, t, table=table, bs=bs: int(table[s, t // bs]) * bs + t % bs
+        got = _host(out)
+        for s_, T in enumerate(lens):
+            idx = np.array([row_of(s_, t) for t in range(int(T))])
+            kk, vv = k[idx].reshape(-1, HKV, D), v[idx].reshape(-1, HKV, D)
+            qs = np.ascontiguousarray(q[s_].reshape(H, D))
+            ok, msg = gate(f"shared workspace call {i} ({kind}) seq {s_} len {T}", got[s_],
+                           orc.attn_decode(qs, kk, vv, int(T), H, HKV, D),
+                           lambda: orc.attn_f64(qs, kk, vv, int(T), H, HKV, D))
+            assert ok, msg
+    assert ws.status() == 0
