@@ -195,8 +195,9 @@ def bench_stream_ceiling(torch, A, H, HKV, n_layer, ctx, reps=50, seed=1000):
 def bench_project(torch, A, E=2560, H=32, HKV=8, n_layer=36, seed=7000):
     """The decode step's QKV projection at Qwen3-4B shape (ei_qkv_project: attention RMSNorm + the
     fused [Wq|Wk|Wv] GEMV, one token): n_layer launches over separate weights in one graph, for fp32
-    and fp16 weights; GB/s of the weight stream + x + out.  Then the whole decode layer from the
+    and fp16 weights and Q8_0 / Q4_K / Q6_K blocks; GB/s of the weight stream + x + out.  Then the whole decode layer from the
     residual (projection + fused decode step, ctx 4096) per layer."""
+    import numpy as np
     from exactinfer_amd import _capi
     dev = "cuda"
     shape = A.AttnShape(H, HKV)
@@ -246,6 +247,29 @@ def bench_project(torch, A, E=2560, H=32, HKV=8, n_layer=36, seed=7000):
             res["decode_layer_from_residual_f16"] = {"us_per_layer": round(ms2 * 1e3, 3), "bytes": tot,
                                                      "gbs": round(tot / (ms2 * 1e-3) / 1e9, 1)}
         del w
+    # quantised rows in their GGUF block layout: random bytes, block scales set to small finite values
+    qfmt = {8: ("q8_0", 32, 34, (0,)), 12: ("q4_k", 256, 144, (0, 2)), 14: ("q6_k", 256, 210, (208,))}
+    dbytes = torch.tensor(list(np.array([0.01], np.float16).view(np.uint8)), dtype=torch.uint8, device=dev)
+    for wtype, (name, vals, bb, d_offs) in qfmt.items():
+        rb = E // vals * bb
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed + wtype)
+        w = torch.randint(0, 256, (n_layer, n_out * rb), dtype=torch.uint8, device=dev, generator=g)
+        blk = w.view(-1, bb)
+        for off in d_offs:
+            blk[:, off:off + 2] = dbytes
+
+        def run_q():
+            for l in range(n_layer):
+                _capi.call("ei_qkv_project", A._stream(), x[l].data_ptr(), E, 1, E, gam.data_ptr(), 1e-6,
+                           w[l].data_ptr(), wtype, n_out, qkv[l].data_ptr(), n_out)
+
+        ms = graph_ms(torch, run_q, reps=20, warm=3) / n_layer
+        nbytes = n_out * rb + 4.0 * (E + n_out)
+        res[name] = {"kernel_us": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
+                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+        del w, blk
     return res
 
 

@@ -448,10 +448,14 @@ EI_API int ei_qkv_project(ei_stream_t stream, const float* x, long x_stride, int
                           const float* attn_norm, float eps, const void* w, int w_type, int n_out, float* qkv,
                           long qkv_stride) {
     REQUIRE(x && attn_norm && w && qkv, "null pointer argument");
-    REQUIRE(w_type == EI_W_F32 || w_type == EI_W_F16, "w_type %d: EI_W_F32 (0) or EI_W_F16 (1)", w_type);
-    if (ei::qkv_project_pieces(n_embd, w_type == EI_W_F16) == 0)
+    REQUIRE(w_type == EI_W_F32 || w_type == EI_W_F16 || w_type == EI_W_Q8_0 || w_type == EI_W_Q4_K ||
+                w_type == EI_W_Q6_K,
+            "w_type %d: EI_W_F32 (0), EI_W_F16 (1), EI_W_Q8_0 (8), EI_W_Q4_K (12) or EI_W_Q6_K (14)", w_type);
+    if (!ei::qkv_project_built(n_embd, w_type))
         return fail(EI_ERR_UNSUPPORTED,
-                    "n_embd %d: built for 1024, 2048, 2560, 4096 and 5120 (F32) and also 8192 and 10240 (F16)", n_embd);
+                    "n_embd %d, w_type %d: built for 1024, 2048, 2560, 4096 and 5120 (F32); also 8192 and 10240 (F16); "
+                    "1024, 2048, 2560, 4096 and 5120 (Q8_0, Q4_K, Q6_K)",
+                    n_embd, w_type);
     REQUIRE(rows >= 0 && rows <= ei::qkv_project_max_rows(n_embd), "rows %d: at most %d rows per launch at n_embd %d",
             rows, ei::qkv_project_max_rows(n_embd), n_embd);
     REQUIRE(n_out > 0, "n_out %d", n_out);
@@ -461,7 +465,7 @@ EI_API int ei_qkv_project(ei_stream_t stream, const float* x, long x_stride, int
             "x, w, attn_norm and x_stride must be 16-byte aligned");
     if (rows == 0) return ok();
     return hip_status(ei::launch_qkv_project(static_cast<hipStream_t>(stream), x, x_stride, rows, n_embd, attn_norm,
-                                             eps, w, w_type == EI_W_F16, n_out, qkv, qkv_stride),
+                                             eps, w, w_type, n_out, qkv, qkv_stride),
                       "qkv projection launch");
 }
 

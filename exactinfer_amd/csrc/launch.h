@@ -115,9 +115,9 @@ hipError_t decode_scratch(void** ptr);
 // attention RMSNorm of B activation rows + the fused QKV product (raw [Q|K|V] rows out)
 constexpr int kProjMaxRows = 4;
 int qkv_project_max_rows(int E);                // rows per launch at hidden size E
-int qkv_project_pieces(int E, bool w_f16);      // 0 when hidden size E is not built
+bool qkv_project_built(int E, int w_type);      // a kernel exists for hidden size E and this weight type
 hipError_t launch_qkv_project(hipStream_t st, const float* x, long x_stride, int B, int E, const float* gamma,
-                              float eps, const void* w, bool w_f16, int n_out, float* out, long out_stride);
+                              float eps, const void* w, int w_type, int n_out, float* out, long out_stride);
 
 // ------------------------------------------------------------------ prefill.hip
 // Key split across workgroups for short chunks: ksplit shares per query block, merged by a

@@ -54,19 +54,26 @@ int ei_abi_version(void);
 int ei_rope_table_fill(float* cs_host, int n_ctx, int rope_dim, double theta);
 
 /* ------------------------------------------------------------------ QKV projection
- * Weight element types of ei_qkv_project (the GGML type ids of F32 and F16). */
-enum { EI_W_F32 = 0, EI_W_F16 = 1 };
+ * Weight element types of ei_qkv_project: the GGML type ids of F32, F16 and of the block
+ * formats the reference decodes (src/quant.h:21-39): Q8_0 (32 values in 34 bytes), Q4_K and
+ * Q6_K (256 values in 144 and 210 bytes). */
+enum { EI_W_F32 = 0, EI_W_F16 = 1, EI_W_Q8_0 = 8, EI_W_Q4_K = 12, EI_W_Q6_K = 14 };
 
 /* Attention RMSNorm + fused QKV projection of `rows` activation rows (decode: one token per
  * sequence): h = rmsnorm(x_b, attn_norm, eps) (sum of squares in double, as the CPU rmsnorm),
  * then qkv_b[r] = sum_i W[r][i] h[i] for the n_out = (n_head + 2 n_head_kv) * 128 rows of the
- * fused [Wq | Wk | Wv] weight (row r of n_embd contiguous elements, F32 or F16 as w_type).
+ * fused [Wq | Wk | Wv] weight (row r of n_embd elements in the GGUF row layout of w_type:
+ * n_embd floats, binary16 values, or n_embd / 32 Q8_0 blocks, n_embd / 256 Q4_K or Q6_K
+ * blocks, rows one after another).  Quantised weights are decoded exactly as the CPU path's
+ * convert_row (src/quant.cpp:7-60).  A file whose Wq, Wk and Wv have different types takes one
+ * call per segment, qkv offset to the segment's first column.
  * Row b of x at x + b*x_stride, of qkv at qkv + b*qkv_stride, left raw: the decode steps
  * (ei_decode_step, ei_decode_step_paged) apply the QK-norm, RoPE and cache append to it.
  * Replaces k_rmsnorm + linear(h, L.qkv, qkv, ...) of src/cuda/model_cuda.cu:1797-1799 (the
  * B == 1 GEMV, :300-320); arithmetic of the CPU path's rmsnorm + matvec (src/ops.cpp:126-160).
  * Built for n_embd 1024, 2048, 2560, 4096, 5120 (every dense Qwen3; F16 also 8192, 10240);
- * 0 <= rows <= min(4, 24576 / n_embd). */
+ * 0 <= rows <= min(4, 24576 / n_embd).
+ * w must be 16-byte aligned (GGUF aligns tensor data to 32 bytes). */
 int ei_qkv_project(ei_stream_t stream, const float* x, long x_stride, int rows, int n_embd, const float* attn_norm,
                    float eps, const void* w, int w_type, int n_out, float* qkv, long qkv_stride);
 

@@ -31,6 +31,10 @@
  *   orc_dot_f32,         (src/ops.cpp:22-24, :92-118) compiled from source (oracle/_ref),
  *   orc_dot_f16          on every binary16 pattern and on dot lengths with and without
  *                        tails; orc_matvec + float64 bound.
+ *   orc_dequant_q8_0,    bit-exact vs the reference's own dequant_q8_0 / _q4_K / _q6_K
+ *   orc_dequant_q4_K,    (src/quant.cpp:7-60) compiled from source (oracle/_ref), on random
+ *   orc_dequant_q6_K     blocks; committed golden vectors; closed forms (unit scales give
+ *                        the stored integers back).
  *   orc_fill_normal      synthetic-input generator (not a reference function): exact
  *                        integer arithmetic, checked for moments and against the GPU fill.
  */
@@ -365,12 +369,118 @@ ORC_API float orc_dot_f16(const uint16_t* w, const float* x, long n) {
     return s;
 }
 
-/* matvec for F32 (type 0) and F16 (type 1) weights (src/ops.cpp:126-153): y[r] = row r . x,
- * rows of n elements stored one after another (GGUF ne[0] = n is the contiguous dimension). */
+/* ------------------------------------------------------------------ quantised rows
+ * GGML block formats the reference computes with (src/quant.h:21-39), decoded to float in the
+ * reference's operation order (src/quant.cpp:7-60); a row of n values is n / block_size blocks
+ * one after another.
+ *   Q8_0 (type 8):  32 values in 34 bytes: binary16 d, 32 int8 q;       y = q * d
+ *   Q4_K (type 12): 256 values in 144 bytes: binary16 d, dmin, 12 bytes of packed 6-bit
+ *                   (scale, min) for 8 sub-blocks of 32, 128 bytes of nibbles;
+ *                   y = (d * sc) * q - dmin * m
+ *   Q6_K (type 14): 256 values in 210 bytes: 128 bytes of low nibbles, 64 of high 2-bit
+ *                   pairs, 16 int8 scales, binary16 d;  y = (d * sc) * (q - 32)          */
+static uint16_t orc_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+ORC_API void orc_dequant_q8_0(const uint8_t* src, float* y, long n) {
+    for (long b = 0; b < n / 32; ++b) {
+        const uint8_t* blk = src + 34 * b;
+        const float d = orc_f16_to_f32(orc_u16(blk));
+        for (int j = 0; j < 32; ++j) y[32 * b + j] = (float)(int8_t)blk[2 + j] * d;
+    }
+}
+
+/* the 6-bit scale and min of sub-block j (0..7) from the 12 packed bytes (src/quant.h:43-52):
+ * j < 4 keeps the low 6 bits of bytes j and j+4; j >= 4 joins the nibbles of byte j+4 with the
+ * top two bits of bytes j-4 (scale) and j (min) */
+static void orc_q4k_sm(const uint8_t* q, int j, int* sc, int* m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+ORC_API void orc_dequant_q4_K(const uint8_t* src, float* y, long n) {
+    for (long b = 0; b < n / 256; ++b) {
+        const uint8_t* blk = src + 144 * b;
+        const float d = orc_f16_to_f32(orc_u16(blk)), dmin = orc_f16_to_f32(orc_u16(blk + 2));
+        const uint8_t* packed = blk + 4;
+        const uint8_t* qs = blk + 16;
+        float* out = y + 256 * b;
+        /* chunk c of 64 values: sub-block 2c from the low nibbles of 32 bytes, 2c+1 from their
+         * high nibbles */
+        for (int c = 0; c < 4; ++c) {
+            for (int half = 0; half < 2; ++half) {
+                int sc, m;
+                orc_q4k_sm(packed, 2 * c + half, &sc, &m);
+                const float dl = d * (float)sc, ml = dmin * (float)m;
+                for (int l = 0; l < 32; ++l) {
+                    const int q = half ? qs[32 * c + l] >> 4 : qs[32 * c + l] & 15;
+                    out[64 * c + 32 * half + l] = dl * (float)q - ml;
+                }
+            }
+        }
+    }
+}
+
+ORC_API void orc_dequant_q6_K(const uint8_t* src, float* y, long n) {
+    for (long b = 0; b < n / 256; ++b) {
+        const uint8_t* blk = src + 210 * b;
+        const float d = orc_f16_to_f32(orc_u16(blk + 208));
+        float* out = y + 256 * b;
+        /* value v = 128 h + 32 g + l (g = 0..3, l = 0..31): the low nibble (g = 0, 1) or the high
+         * nibble (g = 2, 3) of ql[64 h + l + 32 (g & 1)], bits 2g, 2g+1 of qh[32 h + l] on top,
+         * scale scales[8 h + l / 16 + 2 g] */
+        for (int h = 0; h < 2; ++h)
+            for (int g = 0; g < 4; ++g)
+                for (int l = 0; l < 32; ++l) {
+                    const uint8_t lo = blk[64 * h + l + 32 * (g & 1)];
+                    const int nib = g < 2 ? lo & 15 : lo >> 4;
+                    const int hi = (blk[128 + 32 * h + l] >> (2 * g)) & 3;
+                    const int q = (nib | (hi << 4)) - 32;
+                    const int sc = (int8_t)blk[192 + 8 * h + l / 16 + 2 * g];
+                    out[128 * h + 32 * g + l] = d * (float)sc * (float)q;
+                }
+    }
+}
+
+/* bytes of one row of n values */
+ORC_API long orc_row_bytes(int type, long n) {
+    switch (type) {
+        case 0: return 4 * n;
+        case 1: return 2 * n;
+        case 8: return n / 32 * 34;
+        case 12: return n / 256 * 144;
+        case 14: return n / 256 * 210;
+        default: return 0;
+    }
+}
+
+/* matvec (src/ops.cpp:126-153): y[r] = row r . x, rows stored one after another (GGUF ne[0] =
+ * n is the contiguous dimension).  F32 (type 0) and F16 (type 1) rows go through dot_f32 /
+ * dot_f16; quantised rows are decoded into a float buffer first, then dot_f32 (the reference's
+ * convert_row + dot_f32 path). */
 ORC_API void orc_matvec(int type, const void* w, const float* x, float* y, long rows, long n) {
-#pragma omp parallel for schedule(static)
-    for (long r = 0; r < rows; ++r)
-        y[r] = type == 0 ? orc_dot_f32((const float*)w + r * n, x, n) : orc_dot_f16((const uint16_t*)w + r * n, x, n);
+    const long rb = orc_row_bytes(type, n);
+#pragma omp parallel
+    {
+        float* buf = (type == 0 || type == 1) ? NULL : (float*)malloc((size_t)n * sizeof(float));
+#pragma omp for schedule(static)
+        for (long r = 0; r < rows; ++r) {
+            const uint8_t* row = (const uint8_t*)w + r * rb;
+            if (type == 0) y[r] = orc_dot_f32((const float*)row, x, n);
+            else if (type == 1) y[r] = orc_dot_f16((const uint16_t*)row, x, n);
+            else {
+                if (type == 8) orc_dequant_q8_0(row, buf, n);
+                else if (type == 12) orc_dequant_q4_K(row, buf, n);
+                else orc_dequant_q6_K(row, buf, n);
+                y[r] = orc_dot_f32(buf, x, n);
+            }
+        }
+        free(buf);
+    }
 }
 
 /* ------------------------------------------------------------------ float64 brute force

@@ -66,6 +66,10 @@ def lib():
         L.orc_dot_f16.argtypes = [_u16p, _f32p, _c_long]
         L.orc_dot_f16.restype = _c_float
         L.orc_matvec.argtypes = [_c_int, ctypes.c_void_p, _f32p, _f32p, _c_long, _c_long]
+        for name in ("orc_dequant_q8_0", "orc_dequant_q4_K", "orc_dequant_q6_K"):
+            getattr(L, name).argtypes = [ctypes.c_void_p, _f32p, _c_long]
+        L.orc_row_bytes.argtypes = [_c_int, _c_long]
+        L.orc_row_bytes.restype = _c_long
         L.orc_threads.restype = _c_int
         L.orc_set_threads.argtypes = [_c_int]
         _lib = L
@@ -87,6 +91,8 @@ def ref_lib():
             R.elref_dot_f32.restype = _c_float
             R.elref_dot_f16.argtypes = [_u16p, _f32p, _c_long]
             R.elref_dot_f16.restype = _c_float
+            for name in ("elref_dequant_q8_0", "elref_dequant_q4_K", "elref_dequant_q6_K"):
+                getattr(R, name).argtypes = [ctypes.c_void_p, _f32p, _c_long]
         _ref = R
     return _ref
 
@@ -214,7 +220,47 @@ def env_threads() -> int:
 
 
 # ---------------------------------------------------------------- QKV projection
-W_F32, W_F16 = 0, 1
+W_F32, W_F16, W_Q8_0, W_Q4_K, W_Q6_K = 0, 1, 8, 12, 14
+# values per block and bytes per block of the quantised row formats (src/quant.h:21-39)
+QBLOCK = {W_Q8_0: (32, 34), W_Q4_K: (256, 144), W_Q6_K: (256, 210)}
+
+
+def row_bytes(wtype: int, n: int) -> int:
+    return int(lib().orc_row_bytes(wtype, n))
+
+
+def dequant(wtype: int, blocks, n: int) -> np.ndarray:
+    """A quantised row (or rows, as uint8 bytes) of n values each decoded to float32
+    (src/quant.cpp:7-60); blocks holds rows * row_bytes bytes."""
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    out = np.empty(b.size // row_bytes(wtype, n) * n, np.float32)
+    name = {W_Q8_0: "orc_dequant_q8_0", W_Q4_K: "orc_dequant_q4_K", W_Q6_K: "orc_dequant_q6_K"}[wtype]
+    getattr(lib(), name)(b.ctypes.data, out, out.size)
+    return out
+
+
+def random_blocks(wtype: int, rows: int, n: int, seed: int, d_scale: float = 1.0) -> np.ndarray:
+    """Random quantised rows [rows][row_bytes] (uint8): every byte random except the binary16
+    block scales, drawn as moderate positive and negative values (d_scale x 2^-7..2^-4) so the
+    decoded weights stay finite and O(d_scale)."""
+    qk, bb = QBLOCK[wtype]
+    rng = np.random.default_rng(seed)
+    nb = rows * (n // qk)
+    blk = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    def f16(k):
+        v = (rng.uniform(2.0 ** -7, 2.0 ** -4, nb) * rng.choice([-1.0, 1.0], nb) * d_scale).astype(np.float16)
+        return v.view(np.uint16)
+    def put(off, h):
+        blk[:, off] = (h & 0xFF).astype(np.uint8)
+        blk[:, off + 1] = (h >> 8).astype(np.uint8)
+    if wtype == W_Q8_0:
+        put(0, f16(0))
+    elif wtype == W_Q4_K:
+        put(0, f16(0))
+        put(2, np.abs(f16(1).view(np.float16)).astype(np.float16).view(np.uint16))
+    else:
+        put(208, f16(0))
+    return blk.reshape(rows, -1)
 
 
 def f16_to_f32(h) -> np.ndarray:
@@ -233,11 +279,16 @@ def dot(w, x, wtype: int) -> float:
 
 
 def matvec(w, x, wtype: int) -> np.ndarray:
-    """y = W x for W [rows][n] (src/ops.cpp:126-153): float32 weights (W_F32) or binary16
-    patterns as uint16 (W_F16)."""
-    w = np.ascontiguousarray(w, dtype=np.float32 if wtype == W_F32 else np.uint16)
+    """y = W x for W [rows][n] (src/ops.cpp:126-153): float32 weights (W_F32), binary16
+    patterns as uint16 (W_F16), or quantised rows as uint8 bytes [rows][row_bytes]."""
     x = _c(x)
-    rows, n = w.shape
+    n = x.size
+    if wtype in QBLOCK:
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        rows = w.size // row_bytes(wtype, n)
+    else:
+        w = np.ascontiguousarray(w, dtype=np.float32 if wtype == W_F32 else np.uint16)
+        rows, n = w.shape
     y = np.empty(rows, np.float32)
     lib().orc_matvec(wtype, w.ctypes.data, x, y, rows, n)
     return y

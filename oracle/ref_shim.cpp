@@ -9,6 +9,9 @@
 //   elref_f16_to_f32     -> el::f16_to_f32     (src/ops.cpp:22-24)
 //   elref_dot_f32        -> dot_f32            (src/ops.cpp:108-118; file-local, hence the
 //   elref_dot_f16        -> dot_f16             include of ops.cpp into this unit, :92-106)
+//   elref_dequant_q8_0   -> el::dequant_q8_0   (src/quant.cpp:7-13)
+//   elref_dequant_q4_K   -> el::dequant_q4_K   (src/quant.cpp:15-33)
+//   elref_dequant_q6_K   -> el::dequant_q6_K   (src/quant.cpp:35-60)
 //
 // Everything else in those files (CpuModel, read_config, the GGUF tensor table) is left
 // unreferenced and dropped by --gc-sections: it needs src/gguf.cpp, which includes
@@ -16,6 +19,7 @@
 #include "model.cpp"
 #include "ops.cpp"
 #include "ops.h"
+#include "quant.h"
 
 #define REF_API extern "C" __attribute__((visibility("default")))
 
@@ -41,3 +45,9 @@ REF_API float elref_f16_to_f32(uint16_t h) { return el::f16_to_f32(h); }
 REF_API float elref_dot_f32(const float* w, const float* x, long n) { return el::dot_f32(w, x, n); }
 
 REF_API float elref_dot_f16(const uint16_t* w, const float* x, long n) { return el::dot_f16(w, x, n); }
+
+REF_API void elref_dequant_q8_0(const void* src, float* y, long n) { el::dequant_q8_0(src, y, n); }
+
+REF_API void elref_dequant_q4_K(const void* src, float* y, long n) { el::dequant_q4_K(src, y, n); }
+
+REF_API void elref_dequant_q6_K(const void* src, float* y, long n) { el::dequant_q6_K(src, y, n); }

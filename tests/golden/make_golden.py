@@ -11,6 +11,8 @@ compiled from its sources by oracle/Makefile).
   ref_matvec.npz        inputs and outputs of the reference's dot_f32 / dot_f16 (src/ops.cpp:92-118,
                         compiled from source) on seeded rows of lengths with and without tails, and
                         of its f16_to_f32 on every binary16 pattern (as a checksum of the bits).
+  ref_dequant.npz       random Q8_0 / Q4_K / Q6_K rows (every byte random) and the reference's own
+                        dequant_* output for them (src/quant.cpp:7-60, compiled from source).
 
     python tests/golden/make_golden.py
 """
@@ -82,6 +84,14 @@ def main():
     # NaN payloads compare by bits; the checksum covers every pattern's converted bits
     mv["f16_all_bits_sum"] = np.array([int(conv.view(np.uint32).astype(np.uint64).sum())], np.uint64)
     np.savez_compressed(HERE / "ref_matvec.npz", **mv)
+    # dequant_q8_0 / _q4_K / _q6_K (src/quant.cpp:7-60) on random bytes: two rows of 512 values
+    dq = {}
+    for t, name in ((O.W_Q8_0, "q8_0"), (O.W_Q4_K, "q4_K"), (O.W_Q6_K, "q6_K")):
+        blocks = np.random.default_rng(6100 + t).integers(0, 256, size=(2, O.row_bytes(t, 512)), dtype=np.uint8)
+        out = np.empty(2 * 512, np.float32)
+        getattr(R, "elref_dequant_" + name)(blocks.ctypes.data, out, out.size)
+        dq[name + "_blocks"], dq[name + "_out"] = blocks, out
+    np.savez_compressed(HERE / "ref_dequant.npz", **dq)
     print("wrote", sorted(p.name for p in HERE.glob("*.npz")))
 
 

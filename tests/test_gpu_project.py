@@ -15,7 +15,8 @@ from tests.parity import ATTN_RTOL, bits_equal, gate
 pytestmark = pytest.mark.gpu
 
 D = 128
-W_F32, W_F16 = 0, 1
+W_F32, W_F16, W_Q8_0, W_Q4_K, W_Q6_K = 0, 1, 8, 12, 14
+QTYPES = [W_Q8_0, W_Q4_K, W_Q6_K]
 
 
 def _dev(a):
@@ -68,6 +69,59 @@ def test_qkv_project_matches_oracle(orc, gpu, wtype, E, H, HKV, rows):
         assert np.max(np.abs(got[b] - exact) / mag) <= 1e-5
 
 
+def _qweights(orc, n_out, E, wtype, seed):
+    """Random quantised rows with moderate block scales, and the floats they decode to."""
+    blocks = orc.random_blocks(wtype, n_out, E, seed, d_scale=0.05)
+    return blocks, orc.dequant(wtype, blocks, E).reshape(n_out, E)
+
+
+@pytest.mark.parametrize("wtype", QTYPES)
+@pytest.mark.parametrize("E,H,HKV,rows", [(2560, 32, 8, 1), (2560, 32, 8, 4), (1024, 16, 8, 2), (4096, 32, 8, 1),
+                                         (5120, 40, 8, 3)])
+def test_qkv_project_quantised_matches_oracle(orc, gpu, wtype, E, H, HKV, rows):
+    """Q8_0 / Q4_K / Q6_K weights in their GGUF block layout: every output within 1e-5 of
+    sum |w h| of the oracle's matvec (decode with the reference's dequant, then dot_f32), and of
+    the float64 product of the decoded weights."""
+    n_out = (H + 2 * HKV) * D
+    x = orc.normal((rows, E), 8700 + E) * np.float32(3.0)
+    gamma = orc.gamma(E, 8701)
+    blocks, wf = _qweights(orc, n_out, E, wtype, 8702 + E + wtype)
+    got = _host(_project(gpu, x, gamma, blocks, wtype, n_out))
+    for b in range(rows):
+        h = orc.rmsnorm(x[b], gamma)
+        ref = orc.matvec(blocks, h, wtype)
+        mag = np.abs(wf.astype(np.float64)) @ np.abs(h.astype(np.float64))
+        err = np.max(np.abs(got[b].astype(np.float64) - ref) / mag)
+        assert err <= 1e-5, f"w_type {wtype} row {b}: max |got - ref| / sum|w h| = {err:.3e}"
+        exact = wf.astype(np.float64) @ h.astype(np.float64)
+        assert np.max(np.abs(got[b] - exact) / mag) <= 1e-5
+
+
+@pytest.mark.parametrize("wtype", QTYPES)
+def test_qkv_project_quantised_decode_bit_exact(orc, gpu, wtype):
+    """One-hot activations isolate single weights: with x = e_i the normed row has one
+    non-zero h_i, every other product is an exact zero, so output r is float(w[r][i] * h_i)
+    exactly.  Four rows per call, 64 calls cover all 256 positions of every super-block (all
+    Q8_0 quarters, Q4_K sub-blocks and nibble halves, Q6_K groups), bit for bit against the
+    reference's own decode."""
+    E, n_out = 1024, 64
+    gamma = orc.gamma(E, 8801)
+    blocks, wf = _qweights(orc, n_out, E, wtype, 8802 + wtype)
+    for start in range(0, 256, 4):
+        cols = [start + i + 256 * (i % (E // 256)) for i in range(4)]  # four super-blocks in turn
+        x = np.zeros((4, E), np.float32)
+        for b, c in enumerate(cols):
+            x[b, c] = np.float32(1.5)
+        got = _host(_project(gpu, x, gamma, blocks, wtype, n_out))
+        for b, c in enumerate(cols):
+            h = orc.rmsnorm(x[b], gamma)
+            want = (wf[:, c] * h[c]).astype(np.float32)
+            g = got[b].copy()
+            g[(g == 0) & (want == 0)] = 0.0  # a zero weight gives a zero of either sign
+            want[want == 0] = 0.0
+            assert bits_equal(g, want), f"w_type {wtype} column {c}"
+
+
 def test_qkv_project_rejects_unbuilt_shapes(gpu):
     import ctypes
     from exactinfer_amd import _capi
@@ -78,9 +132,11 @@ def test_qkv_project_rejects_unbuilt_shapes(gpu):
         _capi.call("ei_qkv_project", None, p, 2560, 5, 2560, p, 1e-6, p, W_F32, 6144, p, 6144)
     with pytest.raises(_capi.EiError, match="w_type"):
         _capi.call("ei_qkv_project", None, p, 2560, 1, 2560, p, 1e-6, p, 7, 6144, p, 6144)
+    with pytest.raises(_capi.EiError, match="n_embd 2304"):  # not a multiple of 512
+        _capi.call("ei_qkv_project", None, p, 2304, 1, 2304, p, 1e-6, p, W_Q4_K, 6144, p, 6144)
 
 
-@pytest.mark.parametrize("wtype", [W_F32, W_F16])
+@pytest.mark.parametrize("wtype", [W_F32, W_F16, W_Q8_0])
 def test_decode_layer_from_residual(orc, gpu, wtype):
     """Qwen3-4B shapes: residual x -> attention RMSNorm + QKV projection -> fused decode step."""
     E, H, HKV, T = 2560, 32, 8, 1000
@@ -88,7 +144,7 @@ def test_decode_layer_from_residual(orc, gpu, wtype):
     n_out = shape.qkv
     x = orc.normal((1, E), 8600)
     gamma = orc.gamma(E, 8601)
-    w = _weights(orc, n_out, E, wtype, 8602)
+    w = _weights(orc, n_out, E, wtype, 8602) if wtype in (W_F32, W_F16) else _qweights(orc, n_out, E, wtype, 8602)[0]
     qg, kg = orc.gamma(D, 8603), orc.gamma(D, 8604)
     k, v = orc.normal((T, HKV * D), 8605), orc.normal((T, HKV * D), 8606)
     kc, vc = _dev(k), _dev(v)

@@ -325,3 +325,71 @@ def test_matvec_is_the_float64_product_within_fp32_rounding(orc):
     # the same bound rejects a matvec missing its last block
     bad = (w[:, :-16].astype(np.float64) @ x[:-16].astype(np.float64))
     assert np.any(np.abs(bad - exact) > 1e-6 * mag)
+
+
+@pytest.mark.parametrize("wtype", [8, 12, 14])
+def test_dequant_matches_reference(orc, wtype):
+    """orc_dequant_q8_0 / _q4_K / _q6_K == the reference's dequant_* (src/quant.cpp:7-60) bit for
+    bit on random blocks (every byte random, scales included): directly where oracle/_ref builds,
+    and through the committed golden vectors."""
+    names = {8: "q8_0", 12: "q4_K", 14: "q6_K"}
+    g = np.load(GOLDEN / "ref_dequant.npz")
+    blocks, want = g[f"{names[wtype]}_blocks"], g[f"{names[wtype]}_out"]
+    n = want.size // blocks.shape[0]
+    assert bits_equal(orc.dequant(wtype, blocks, n), want)
+    R = orc.ref_lib()
+    if R is not None:
+        for seed in range(4):
+            b = np.random.default_rng(9100 + seed).integers(0, 256, size=(3, orc.row_bytes(wtype, 1024)),
+                                                            dtype=np.uint8)
+            ref = np.empty(3 * 1024, np.float32)
+            getattr(R, "elref_dequant_" + names[wtype])(b.ctypes.data, ref, ref.size)
+            assert bits_equal(orc.dequant(wtype, b, 1024), ref)
+
+
+@pytest.mark.parametrize("wtype", [8, 12, 14])
+def test_dequant_closed_forms(orc, wtype):
+    """Block scales of 1 give the stored integers back: Q8_0 q; Q4_K sub-block scale s and min
+    m give s q - m; Q6_K scale s gives s (q - 32).  A transposed nibble, a wrong sub-block or a
+    misplaced high bit changes the integers the bytes spell out."""
+    rng = np.random.default_rng(9200 + wtype)
+    one = np.float16(1.0).view(np.uint16)
+    if wtype == 8:
+        blk = rng.integers(0, 256, size=(1, 34), dtype=np.uint8)
+        blk[0, 0], blk[0, 1] = one & 0xFF, one >> 8
+        assert np.array_equal(orc.dequant(8, blk, 32), blk[0, 2:].view(np.int8).astype(np.float32))
+    elif wtype == 12:
+        blk = rng.integers(0, 256, size=(1, 144), dtype=np.uint8)
+        blk[0, 0], blk[0, 1], blk[0, 2], blk[0, 3] = one & 0xFF, one >> 8, one & 0xFF, one >> 8
+        p = blk[0, 4:16].astype(int)
+        sc = [p[j] & 63 if j < 4 else (p[j + 4] & 15) | ((p[j - 4] >> 6) << 4) for j in range(8)]
+        mn = [p[j + 4] & 63 if j < 4 else (p[j + 4] >> 4) | ((p[j] >> 6) << 4) for j in range(8)]
+        qs = blk[0, 16:].astype(int)
+        want = np.empty(256)
+        for c in range(4):
+            want[64 * c:64 * c + 32] = sc[2 * c] * (qs[32 * c:32 * c + 32] & 15) - mn[2 * c]
+            want[64 * c + 32:64 * c + 64] = sc[2 * c + 1] * (qs[32 * c:32 * c + 32] >> 4) - mn[2 * c + 1]
+        assert np.array_equal(orc.dequant(12, blk, 256), want.astype(np.float32))
+    else:
+        blk = rng.integers(0, 256, size=(1, 210), dtype=np.uint8)
+        blk[0, 208], blk[0, 209] = one & 0xFF, one >> 8
+        ql, qh, scl = blk[0, :128].astype(int), blk[0, 128:192].astype(int), blk[0, 192:208].view(np.int8).astype(int)
+        want = np.empty(256)
+        for v in range(256):
+            h, r = divmod(v, 128)
+            g, l = divmod(r, 32)
+            lo = ql[64 * h + l + 32 * (g & 1)]
+            q = ((lo & 15) if g < 2 else (lo >> 4)) | (((qh[32 * h + l] >> (2 * g)) & 3) << 4)
+            want[v] = scl[8 * h + l // 16 + 2 * g] * (q - 32)
+        assert np.array_equal(orc.dequant(14, blk, 256), want.astype(np.float32))
+
+
+def test_quantised_matvec_is_decode_then_dot_f32(orc):
+    """orc_matvec on quantised rows == dot_f32 of each decoded row (the reference's convert_row +
+    dot_f32, src/ops.cpp:126-153)."""
+    x = orc.normal((2560,), 9300)
+    for wtype in (8, 12, 14):
+        blocks = orc.random_blocks(wtype, 8, 2560, 9310 + wtype)
+        wf = orc.dequant(wtype, blocks, 2560).reshape(8, 2560)
+        y = orc.matvec(blocks, x, wtype)
+        assert bits_equal(y, np.array([orc.dot(wf[r], x, orc.W_F32) for r in range(8)], np.float32))
