@@ -619,6 +619,9 @@ def main():
     if extra or args.only == "stream-ceiling":
         log("stream ceiling of the configs[1] decode plan ...")
         res["stream_ceiling"] = bench_stream_ceiling(torch, A, 32, 8, 36, 4096)
+        lc = bench_stream_ceiling(torch, A, 16, 8, 28, 32768, reps=10)  # configs[3]'s plan (1024-key chunks)
+        res["stream_ceiling"]["longctx"] = {"kernel_ms": round(lc["kernel_ms"], 4), "gbs": round(lc["gbs"], 1),
+                                            "pct_hbm_peak": round(100 * lc["gbs"] / HBM_PEAK_GBS, 2)}
         log(json.dumps(res["stream_ceiling"]))
     if extra or args.only == "project":
         log("QKV projection at Qwen3-4B shape ...")
