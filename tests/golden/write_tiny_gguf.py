@@ -3,8 +3,8 @@
 No Qwen3 GGUF exists in this environment, so the reader and the end-to-end harness are exercised
 on files this script writes from tests/tiny_qwen3.py's seeded random weights: the tensor names,
 shapes and metadata keys a Qwen3 GGUF carries (read_config / read_tensors, src/model.cpp:38-103),
-F32 or F16 weights (norm vectors stay F32), GGUF version 3, the data section aligned to
-general.alignment.  The writer is independent of the reader under test (plain struct packing).
+F32 or F16 weights (norm vectors stay F32), or any tensor given as raw GGML blocks (Quantised),
+GGUF version 3, the data section aligned to general.alignment.  The writer is independent of the reader under test (plain struct packing).
 
     python tests/golden/write_tiny_gguf.py OUT.gguf [--f16] [--seed N]
 """
@@ -79,8 +79,28 @@ def qwen3_metadata(model, n_ctx: int = 4096, alignment: int = 32) -> list[tuple[
             ("qwen3.attention.layer_norm_rms_epsilon", T_F32, 1e-6)]
 
 
+class Quantised:
+    """A tensor stored in a GGML block format: its type id, ne (ne[0] contiguous) and raw bytes
+    (rows of ne[0] / block_size blocks)."""
+
+    def __init__(self, type_id: int, ne, data: np.ndarray):
+        self.type_id, self.ne = type_id, tuple(int(n) for n in ne)
+        self.data = np.ascontiguousarray(data, dtype=np.uint8)
+        self.nbytes = self.data.nbytes
+
+    def tobytes(self) -> bytes:
+        return self.data.tobytes()
+
+
+def _type_and_ne(a):
+    if isinstance(a, Quantised):
+        return a.type_id, a.ne
+    return (1 if a.dtype == np.float16 else 0), a.shape[::-1]
+
+
 def write_gguf(path, metadata, tensors, alignment: int = 32, version: int = 3) -> None:
-    """metadata: (key, type id, value); tensors: (name, array) with ne = array.shape[::-1]."""
+    """metadata: (key, type id, value); tensors: (name, array) with ne = array.shape[::-1], or
+    (name, Quantised)."""
     head = struct.pack("<IIQQ", 0x46554747, version, len(tensors), len(metadata))
     head += b"".join(_kv(k, t, v) for k, t, v in metadata)
     offsets, off = [], 0
@@ -88,8 +108,8 @@ def write_gguf(path, metadata, tensors, alignment: int = 32, version: int = 3) -
         offsets.append(off)
         off += (a.nbytes + alignment - 1) // alignment * alignment
     for (name, a), o in zip(tensors, offsets):
-        ty = 1 if a.dtype == np.float16 else 0
-        head += _s(name) + struct.pack("<I", a.ndim) + b"".join(struct.pack("<Q", n) for n in a.shape[::-1])
+        ty, ne = _type_and_ne(a)
+        head += _s(name) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<Q", n) for n in ne)
         head += struct.pack("<IQ", ty, o)
     pad = (-len(head)) % alignment
     with open(path, "wb") as f:

@@ -12,7 +12,7 @@ import struct
 import numpy as np
 import pytest
 
-from tests.golden.write_tiny_gguf import T_STRING, T_U32, qwen3_metadata, qwen3_tensors, write_gguf
+from tests.golden.write_tiny_gguf import T_STRING, T_U32, Quantised, qwen3_metadata, qwen3_tensors, write_gguf
 from tests.tiny_qwen3 import TinyQwen3, oracle_attention, run_sequence
 
 
@@ -199,3 +199,46 @@ def test_qwen3_validation(tmp_path, model):
     # a tied embedding (no output.weight) is accepted
     with GgufFile(_write(tmp_path, model, name="tied.gguf", tensors=[t for t in tens if t[0] != "output.weight"])) as g:
         assert g.qwen3_config()["n_vocab"] == model.V
+
+
+def mixed_type_file(tmp_path, orc, E=1024, H=8, HKV=2, seed=8900):
+    """A one-layer Qwen3 file in the layout of a Q4_K_M quantisation: Wq Q4_K, Wk Q8_0, Wv Q6_K
+    (random blocks with moderate scales), the rest F32.  Returns the path and the q/k/v blocks."""
+    D, FF, V = 128, 512, 256
+    rng = np.random.default_rng(seed)
+    f = lambda *shape: rng.standard_normal(shape).astype(np.float32) * np.float32(0.05)
+    q = orc.random_blocks(orc.W_Q4_K, H * D, E, seed + 1, d_scale=0.05)
+    k = orc.random_blocks(orc.W_Q8_0, HKV * D, E, seed + 2, d_scale=0.05)
+    v = orc.random_blocks(orc.W_Q6_K, HKV * D, E, seed + 3, d_scale=0.05)
+    tens = [("token_embd.weight", f(V, E)), ("output_norm.weight", np.ones(E, np.float32)),
+            ("blk.0.attn_norm.weight", np.ones(E, np.float32)),
+            ("blk.0.attn_q.weight", Quantised(orc.W_Q4_K, (E, H * D), q)),
+            ("blk.0.attn_k.weight", Quantised(orc.W_Q8_0, (E, HKV * D), k)),
+            ("blk.0.attn_v.weight", Quantised(orc.W_Q6_K, (E, HKV * D), v)),
+            ("blk.0.attn_q_norm.weight", np.ones(D, np.float32)), ("blk.0.attn_k_norm.weight", np.ones(D, np.float32)),
+            ("blk.0.attn_output.weight", f(E, H * D)), ("blk.0.ffn_norm.weight", np.ones(E, np.float32)),
+            ("blk.0.ffn_gate.weight", f(FF, E)), ("blk.0.ffn_up.weight", f(FF, E)), ("blk.0.ffn_down.weight", f(E, FF))]
+
+    class M:
+        pass
+    m = M()
+    m.n_layer, m.E, m.H, m.HKV = 1, E, H, HKV
+    m.layers = [{"wg": np.zeros((FF, 1))}]
+    p = tmp_path / "mixed.gguf"
+    write_gguf(p, qwen3_metadata(m), tens)
+    return p, q, k, v
+
+
+def test_quantised_tensors_read_back(tmp_path, orc):
+    """Q4_K / Q8_0 / Q6_K tensors: the reader accepts the Qwen3 table with these types and hands
+    back each tensor's bytes as written, [rows][row bytes]."""
+    from exactinfer_amd.gguf import GgufFile
+    p, q, k, v = mixed_type_file(tmp_path, orc)
+    with GgufFile(p) as g:
+        c = g.qwen3_config()
+        assert (c["n_embd"], c["n_head"], c["n_head_kv"]) == (1024, 8, 2)
+        for name, want, ty in (("blk.0.attn_q.weight", q, 12), ("blk.0.attn_k.weight", k, 8),
+                               ("blk.0.attn_v.weight", v, 14)):
+            got = g.tensor(name)
+            assert got.dtype == np.uint8 and got.shape == want.shape and np.array_equal(got, want), name
+            assert g.tensor_info(name)[0] == ty

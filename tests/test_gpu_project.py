@@ -178,3 +178,37 @@ def test_decode_layer_from_residual(orc, gpu, wtype):
                                 rv2.reshape(T, HKV, D), T, H, HKV, D)
     from tests.parity import rel_err
     assert rel_err(out.reshape(H, D), ref_chain) <= 20 * ATTN_RTOL
+
+
+def test_projection_from_gguf_mixed_types(orc, gpu, tmp_path):
+    """The path a real quantised model takes: a file with Wq Q4_K, Wk Q8_0, Wv Q6_K (the layout
+    of a Q4_K_M quantisation) read through the GGUF reader, each segment's mapped bytes uploaded
+    as they are and projected into its columns of the QKV row (one call per segment), against the
+    oracle's decode + matvec of the same bytes."""
+    import torch
+    from exactinfer_amd import _capi
+    from exactinfer_amd.gguf import GgufFile
+    from tests.test_gguf import mixed_type_file
+    E, H, HKV = 1024, 8, 2
+    p, _, _, _ = mixed_type_file(tmp_path, orc, E, H, HKV)
+    x = orc.normal((1, E), 8950) * np.float32(2.0)
+    gamma = orc.gamma(E, 8951)
+    n_out = (H + 2 * HKV) * D
+    qkv = torch.full((1, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    xd, gd = _dev(x), _dev(gamma)
+    h = orc.rmsnorm(x[0], gamma)
+    with GgufFile(p) as g:
+        col = 0
+        for name, rows in (("blk.0.attn_q.weight", H * D), ("blk.0.attn_k.weight", HKV * D),
+                           ("blk.0.attn_v.weight", HKV * D)):
+            blocks = g.tensor(name)
+            wtype = g.tensor_info(name)[0]
+            wd = _dev(blocks)
+            _capi.call("ei_qkv_project", gpu._stream(), xd.data_ptr(), E, 1, E, gd.data_ptr(), 1e-6, wd.data_ptr(),
+                       wtype, rows, qkv[:, col:].data_ptr(), n_out)
+            got = _host(qkv)[0, col:col + rows]
+            ref = orc.matvec(blocks, h, wtype)
+            wf = orc.dequant(wtype, blocks, E).reshape(rows, E).astype(np.float64)
+            mag = np.abs(wf) @ np.abs(h.astype(np.float64))
+            assert np.max(np.abs(got.astype(np.float64) - ref) / mag) <= 1e-5, name
+            col += rows
