@@ -557,21 +557,31 @@ __global__ __launch_bounds__(128) void k_prefill_combine(const float* __restrict
                                                          int rows, int ksplit) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 5), d4 = threadIdx.x & 31;
     if (row >= rows) return;
+    // every share's (m, l) and accumulator piece is loaded before any is used: one round trip
+    float2 ml[kPrefillMaxSplit];
+    float4 v[kPrefillMaxSplit];
+#pragma unroll
+    for (int s = 0; s < kPrefillMaxSplit; ++s) {
+        if (s >= ksplit) break;
+        const size_t slot = (size_t)s * rows + row;
+        ml[s] = *reinterpret_cast<const float2*>(part_ml + slot * 2);
+        v[s] = *reinterpret_cast<const float4*>(part_o + slot * kHeadDim + 4 * d4);
+    }
     float M = -INFINITY;
-    for (int s = 0; s < ksplit; ++s) M = fmaxf(M, part_ml[((size_t)s * rows + row) * 2]);
+#pragma unroll
+    for (int s = 0; s < kPrefillMaxSplit; ++s)
+        if (s < ksplit) M = fmaxf(M, ml[s].x);
     float L = 0.f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < ksplit; ++s) {
-        const size_t slot = (size_t)s * rows + row;
-        const float2 ml = *reinterpret_cast<const float2*>(part_ml + slot * 2);
-        if (ml.x == -INFINITY) continue;
-        const float wv = __builtin_amdgcn_exp2f(ml.x - M);
-        const float4 v = *reinterpret_cast<const float4*>(part_o + slot * kHeadDim + 4 * d4);
-        L = fmaf(wv, ml.y, L);
-        o.x = fmaf(wv, v.x, o.x);
-        o.y = fmaf(wv, v.y, o.y);
-        o.z = fmaf(wv, v.z, o.z);
-        o.w = fmaf(wv, v.w, o.w);
+#pragma unroll
+    for (int s = 0; s < kPrefillMaxSplit; ++s) {
+        if (s >= ksplit || ml[s].x == -INFINITY) continue;  // an empty share adds nothing
+        const float wv = __builtin_amdgcn_exp2f(ml[s].x - M);
+        L = fmaf(wv, ml[s].y, L);
+        o.x = fmaf(wv, v[s].x, o.x);
+        o.y = fmaf(wv, v[s].y, o.y);
+        o.z = fmaf(wv, v[s].z, o.z);
+        o.w = fmaf(wv, v[s].w, o.w);
     }
     const float inv = 1.f / L;
     o.x *= inv;
