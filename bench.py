@@ -399,11 +399,13 @@ def bench_prefill(torch, A, H, HKV, n_layer, T, steps, warmup, seed=2000):
             "flops_per_launch": flops_layer}
 
 
-def bench_prefill_chunked(torch, A, H, HKV, n_layer, T, chunk, split=True, seed=2100, step=False):
+def bench_prefill_chunked(torch, A, H, HKV, n_layer, T, chunk, split=True, seed=2100, step=False, block_size=0):
     """configs[2]'s prompt as the reference engine feeds it: chunks of `chunk` tokens at pos0 = 0, chunk, ...
     (src/cuda/model_cuda.cu:1912 caps a prefill chunk at 512).  Attention launches only, one graph; with
     step=True the engine's whole chunk path instead (ei_prefill_step: key prologue + attention with q normed
-    in-kernel; replays re-norm the K heads in place, which keeps them bounded)."""
+    in-kernel; replays re-norm the K heads in place, which keeps them bounded).  block_size > 0: the
+    step over a paged pool (each layer's cache rows in shuffled blocks of block_size rows,
+    ei_prefill_step_paged)."""
     shape = A.AttnShape(H, HKV)
     dev = "cuda"
     kd = HKV * D
@@ -416,6 +418,11 @@ def bench_prefill_chunked(torch, A, H, HKV, n_layer, T, chunk, split=True, seed=
     ws = A.PrefillWorkspace(chunk, H, HKV, T) if split else None  # the engine's path: key split for short chunks
     gam = torch.ones((2, D), dtype=torch.float32, device=dev)
     cs = A.rope_table(T, device=dev) if step else None
+    tables = None
+    if block_size:
+        import numpy as np
+        rng = np.random.default_rng(seed + 7)
+        tables = [torch.from_numpy(rng.permutation(T // block_size).astype(np.int32)).to(dev) for _ in range(n_layer)]
 
     def run():
         for l in range(n_layer):
@@ -423,13 +430,14 @@ def bench_prefill_chunked(torch, A, H, HKV, n_layer, T, chunk, split=True, seed=
                 n = min(chunk, T - s)
                 if step:
                     A.prefill_step(q[l, s:s + n], kc[l], vc[l], shape, gam[0], gam[1], cs, p, ws, B=n,
-                                   out=out[l, s:s + n])
+                                   out=out[l, s:s + n], block_table=None if tables is None else tables[l],
+                                   block_size=block_size)
                 else:
                     A.attn_prefill(q[l, s:s + n], kc[l], vc[l], p, shape, B=n, out=out[l, s:s + n], ws=ws)
 
     ms = graph_ms(torch, run, reps=5, warm=1) / n_layer
     flops = A.flops_causal(T, 0, H)
-    key = "step_ms_per_layer" if step else "kernel_ms_per_layer"
+    key = ("paged_step_ms_per_layer" if block_size else "step_ms_per_layer") if step else "kernel_ms_per_layer"
     return {"chunk": chunk, "key_split": split, key: ms, key.replace("ms_per_layer", "tflops"): flops / (ms * 1e-3) / 1e12}
 
 
@@ -588,6 +596,7 @@ def main():
         log("prefill configs[2] in 512-token chunks ...")
         res["prefill_chunked"] = bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512)
         res["prefill_chunked"].update(bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512, step=True))
+        res["prefill_chunked"].update(bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512, step=True, block_size=64))
         log(json.dumps(res["prefill_chunked"]))
         log(json.dumps(bench_prefill_chunked(torch, A, 32, 8, 36, 2048, 512, split=False)))
     if args.only == "decode-groups":  # configs[1]'s decode at the other dense Qwen3 group sizes

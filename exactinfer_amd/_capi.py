@@ -20,7 +20,7 @@ LIB_PATH = Path(os.environ.get("EI_ATTN_LIB") or Path(__file__).resolve().parent
 EXPORTS = (
     "ei_last_error", "ei_abi_version", "ei_rope_table_fill", "ei_headnorm_rope", "ei_kv_append", "ei_qkv_prepare",
     "ei_attn_decode_ws_bytes", "ei_attn_workspace_init", "ei_attn_decode", "ei_attn_decode_batched",
-    "ei_decode_step", "ei_decode_step_noalloc", "ei_attn_decode_paged", "ei_decode_step_paged", "ei_attn_prefill", "ei_attn_prefill_ws_bytes", "ei_attn_prefill_split", "ei_prefill_step", "ei_qkv_project", "ei_stream_ceiling", "ei_synth_fill",
+    "ei_decode_step", "ei_decode_step_noalloc", "ei_attn_decode_paged", "ei_decode_step_paged", "ei_attn_prefill", "ei_attn_prefill_ws_bytes", "ei_attn_prefill_split", "ei_prefill_step", "ei_prefill_step_paged", "ei_qkv_project", "ei_stream_ceiling", "ei_synth_fill",
     # include/ei_gguf.h
     "ei_gguf_open", "ei_gguf_close", "ei_gguf_version", "ei_gguf_n_tensors", "ei_gguf_tensor", "ei_gguf_find_tensor",
     "ei_gguf_get_int", "ei_gguf_get_float", "ei_gguf_get_str", "ei_gguf_qwen3_config",
@@ -51,6 +51,8 @@ _SIGS = {
     "ei_attn_prefill_ws_bytes": ([_i, _i, _i, _i], _sz),
     "ei_attn_prefill_split": ([_vp, _vp, _l, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp, _sz], _i),
     "ei_prefill_step": ([_vp, _vp, _l, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _i, _f, _f, _i, _vp, _sz], _i),
+    "ei_prefill_step_paged": ([_vp, _vp, _l, _vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _i, _f, _f,
+                               _i, _vp, _sz], _i),
     "ei_qkv_project": ([_vp, _vp, _l, _i, _i, _vp, _f, _vp, _i, _i, _vp, _l], _i),
     "ei_gguf_open": ([ctypes.c_char_p], _vp),
     "ei_gguf_close": ([_vp], None),

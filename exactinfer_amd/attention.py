@@ -235,20 +235,27 @@ def attn_prefill(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos_dev: t
 
 def prefill_step(qkv: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, shape: AttnShape, q_gamma: torch.Tensor,
                  k_gamma: torch.Tensor, cs: torch.Tensor, pos_dev: torch.Tensor, ws: PrefillWorkspace,
-                 B: int | None = None, scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                 B: int | None = None, scale: float | None = None, out: torch.Tensor | None = None,
+                 block_table: torch.Tensor | None = None, block_size: int = 0) -> torch.Tensor:
     """Fused chunk step (ei_prefill_step): K heads normed + roped in place and appended with V
     at rows pos..pos+B-1; Q heads left raw in qkv and normed inside the attention kernel.
-    qkv [B, >= (H+2HKV)*128]; returns [B, H, 128]."""
+    qkv [B, >= (H+2HKV)*128]; returns [B, H, 128].  With block_table (int32 [max_blocks]) the
+    caches are a paged pool of block_size-row blocks (ei_prefill_step_paged)."""
     _need_gpu_f32("qkv", qkv)
     B = qkv.shape[0] if B is None else B
     if B > ws.max_B:
         raise ValueError(f"prefill workspace serves chunks of up to {ws.max_B} rows, got B={B}")
     out = torch.empty((B, shape.n_head, HEAD_DIM), dtype=torch.float32, device=qkv.device) if out is None else out
     scale = default_scale() if scale is None else scale
-    _capi.call("ei_prefill_step", _stream(), qkv.data_ptr(), qkv.stride(0), out.data_ptr(), kc.data_ptr(),
-               vc.data_ptr(), pos_dev.data_ptr(), B, shape.n_head, shape.n_head_kv, shape.head_dim,
-               q_gamma.data_ptr(), k_gamma.data_ptr(), cs.data_ptr(), shape.rope_dim, float(shape.eps), float(scale),
-               ws.max_kv, ws.buf.data_ptr(), ws.nbytes)
+    tail = (q_gamma.data_ptr(), k_gamma.data_ptr(), cs.data_ptr(), shape.rope_dim, float(shape.eps), float(scale),
+            ws.max_kv, ws.buf.data_ptr(), ws.nbytes)
+    if block_table is None:
+        _capi.call("ei_prefill_step", _stream(), qkv.data_ptr(), qkv.stride(0), out.data_ptr(), kc.data_ptr(),
+                   vc.data_ptr(), pos_dev.data_ptr(), B, shape.n_head, shape.n_head_kv, shape.head_dim, *tail)
+    else:
+        _capi.call("ei_prefill_step_paged", _stream(), qkv.data_ptr(), qkv.stride(0), out.data_ptr(), kc.data_ptr(),
+                   vc.data_ptr(), block_table.data_ptr(), block_table.numel(), block_size, pos_dev.data_ptr(), B,
+                   shape.n_head, shape.n_head_kv, shape.head_dim, *tail)
     return out
 
 

@@ -411,10 +411,12 @@ EI_API int ei_attn_prefill_split(ei_stream_t stream, const float* q, long q_stri
                       "prefill launch");
 }
 
-EI_API int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, float* out, float* kc, float* vc,
-                           const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim, const float* q_gamma,
-                           const float* k_gamma, const float* cs, int rope_dim, float eps, float scale, int max_kv,
-                           void* ws, size_t ws_bytes) {
+namespace {
+
+int prefill_step_impl(ei_stream_t stream, float* qkv, long row_stride, float* out, float* kc, float* vc,
+                      const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim, const float* q_gamma,
+                      const float* k_gamma, const float* cs, int rope_dim, float eps, float scale, int max_kv, void* ws,
+                      size_t ws_bytes, const int* block_table, int block_shift) {
     if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
     if (int e = check_rope(rope_dim, head_dim)) return e;
     REQUIRE(qkv && out && kc && vc && pos_dev && q_gamma && k_gamma && cs, "null pointer argument");
@@ -434,14 +436,43 @@ EI_API int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, floa
     // split over at most two shares: each share norms the q rows it stages, so with more shares
     // the repeated norm costs more than the q traffic it saves in the prologue (measured on
     // 512-token chunks with 4 shares); otherwise the prologue norms every head in place first
-    const bool fuse_q = rope_dim == head_dim && ksplit <= 2;
+    // (the paged variant always takes the full prologue: the in-kernel norm and the block table
+    // together exceed the attention kernel's register budget)
+    const bool fuse_q = rope_dim == head_dim && ksplit <= 2 && block_table == nullptr;
     if (int e = hip_status(ei::launch_qkv_prepare(st, qkv, B, row_stride, n_head, n_head_kv, q_gamma, k_gamma, cs,
-                                                  pos_dev, rope_dim, eps, kc, vc, fuse_q ? n_head : 0),
+                                                  pos_dev, rope_dim, eps, kc, vc, fuse_q ? n_head : 0, block_table,
+                                                  block_shift),
                            "prefill step: prologue launch"))
         return e;
     return hip_status(ei::launch_prefill(st, qkv, row_stride, out, kc, vc, pos_dev, B, n_head, n_head_kv, scale, ksplit,
-                                         ws, fuse_q ? q_gamma : nullptr, cs, eps),
+                                         ws, fuse_q ? q_gamma : nullptr, cs, eps, block_table, block_shift),
                       "prefill step: attention launch");
+}
+
+}  // namespace
+
+EI_API int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, float* out, float* kc, float* vc,
+                           const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim, const float* q_gamma,
+                           const float* k_gamma, const float* cs, int rope_dim, float eps, float scale, int max_kv,
+                           void* ws, size_t ws_bytes) {
+    return prefill_step_impl(stream, qkv, row_stride, out, kc, vc, pos_dev, B, n_head, n_head_kv, head_dim, q_gamma,
+                             k_gamma, cs, rope_dim, eps, scale, max_kv, ws, ws_bytes, nullptr, 0);
+}
+
+EI_API int ei_prefill_step_paged(ei_stream_t stream, float* qkv, long row_stride, float* out, float* kc, float* vc,
+                                 const int* block_table, int max_blocks, int block_size, const int* pos_dev, int B,
+                                 int n_head, int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma,
+                                 const float* cs, int rope_dim, float eps, float scale, int max_kv, void* ws,
+                                 size_t ws_bytes) {
+    REQUIRE(block_table != nullptr, "null block_table");
+    REQUIRE(block_size >= 32 && (block_size & (block_size - 1)) == 0,
+            "block_size %d must be a power of two >= 32 (whole 32-key prefill tiles per block)", block_size);
+    REQUIRE(max_blocks > 0 && (long)max_blocks * block_size >= max_kv,
+            "max_blocks %d x block_size %d does not cover max_kv %d", max_blocks, block_size, max_kv);
+    int shift = 0;
+    while ((1 << shift) < block_size) ++shift;
+    return prefill_step_impl(stream, qkv, row_stride, out, kc, vc, pos_dev, B, n_head, n_head_kv, head_dim, q_gamma,
+                             k_gamma, cs, rope_dim, eps, scale, max_kv, ws, ws_bytes, block_table, shift);
 }
 
 EI_API int ei_qkv_project(ei_stream_t stream, const float* x, long x_stride, int rows, int n_embd,

@@ -146,7 +146,9 @@ __device__ __forceinline__ void norm_rope_q8(float* row, const float (&g)[16], c
     }
 }
 
-template <bool kNormQ>
+// kPaged: key t of the sequence sits in pool row btab[t >> bshift] << bshift | (t & mask), the
+// block size 2^bshift >= 32, so a 32-key tile lies in one block and its rows are consecutive.
+template <bool kNormQ, bool kPaged>
 __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __restrict__ q, long q_stride,
                                                            float* __restrict__ out, const float* __restrict__ kc,
                                                            const float* __restrict__ vc,
@@ -154,7 +156,8 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
                                                            float scale, int ksplit,
                                                            float* __restrict__ part_o, float* __restrict__ part_ml,
                                                            const float* __restrict__ q_gamma,
-                                                           const float2* __restrict__ cs, float eps) {
+                                                           const float2* __restrict__ cs, float eps,
+                                                           const int* __restrict__ btab, int bshift) {
     constexpr int D = kHeadDim;
     constexpr int GW = kSlots;
     constexpr int DMA_PER_WAVE = 16 / GW;  // V DMA instructions per wave per tile (K: twice as many, 32 lanes each)
@@ -177,6 +180,11 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
     const float* vbase = vc + (size_t)kvh * D;
     const uint64_t kb_bytes = (uint64_t)(uintptr_t)kbase, vb_bytes = (uint64_t)(uintptr_t)vbase;
     const uint32_t row_bytes = (uint32_t)(KD * sizeof(float));          // one cache row (all KV heads)
+    // cache row of key t (wave-uniform t: one scalar load of the block table when paged)
+    auto crow = [&](int t) -> uint32_t {
+        if constexpr (kPaged) return ((uint32_t)btab[t >> bshift] << bshift) | ((uint32_t)t & ((1u << bshift) - 1u));
+        else return (uint32_t)t;
+    };
     const uint32_t voff_k = 16u * col;                                  // K: lanes 0..31, one row
     const uint32_t voff_v = (uint32_t)hh * row_bytes + 16u * col;        // V: two rows per instruction
     const int nb = (B + kQB - 1) / kQB;
@@ -301,8 +309,9 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
             const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsm + buf * kKTileF));
             const int r0 = hw * 2 * DMA_PER_WAVE;  // this wave's first row of the tile
             if (hh == 0) {
+                const uint32_t row0 = crow(t0);  // the tile's rows are consecutive from here
                 if (t0 + kKT <= T) {
-                    const uint64_t sb = kb_bytes + (uint64_t)(uint32_t)(t0 + r0) * row_bytes;
+                    const uint64_t sb = kb_bytes + (uint64_t)(row0 + r0) * row_bytes;
 #pragma unroll
                     for (int j = 0; j < 2 * DMA_PER_WAVE; ++j)  // one padded row per instruction
                         dma16_s(sb + (uint64_t)j * row_bytes, voff_k, lb + (r0 + j) * (kKS_F * 4));
@@ -310,7 +319,7 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
 #pragma unroll
                     for (int j = 0; j < 2 * DMA_PER_WAVE; ++j) {
                         const int key = min(t0 + r0 + j, T - 1);
-                        dma16(kbase + (size_t)key * KD + 4 * col, lb + (r0 + j) * (kKS_F * 4));
+                        dma16(kbase + (size_t)(row0 + (key - t0)) * KD + 4 * col, lb + (r0 + j) * (kKS_F * 4));
                     }
                 }
             }
@@ -319,8 +328,9 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
             const int t0 = (kt_lo + kKS * i + grp) * kKT;
             const uint32_t lb = __builtin_amdgcn_readfirstlane(lds_addr(gsv + buf * kVTileF));
             const int i0 = hw * DMA_PER_WAVE;  // 1 KB instruction = keys 2*ins, 2*ins+1
+            const uint32_t row0 = crow(t0);
             if (t0 + kKT <= T) {
-                const uint64_t sb = vb_bytes + (uint64_t)(uint32_t)(t0 + 2 * i0) * row_bytes;
+                const uint64_t sb = vb_bytes + (uint64_t)(row0 + 2 * i0) * row_bytes;
 #pragma unroll
                 for (int j = 0; j < DMA_PER_WAVE; ++j)
                     dma16_s(sb + (uint64_t)(2 * j) * row_bytes, voff_v, lb + (i0 + j) * 1024);
@@ -328,7 +338,7 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
 #pragma unroll
                 for (int j = 0; j < DMA_PER_WAVE; ++j) {
                     const int key = min(t0 + 2 * (i0 + j) + hh, T - 1);
-                    dma16(vbase + (size_t)key * KD + 4 * col, lb + (i0 + j) * 1024);
+                    dma16(vbase + (size_t)(row0 + (key - t0)) * KD + 4 * col, lb + (i0 + j) * 1024);
                 }
             }
         };
@@ -474,14 +484,31 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
             __syncthreads();
             if (n_mine > 0) qk(gsm, sa);
         }
+        // paged: the cache row of the K tile fetched at iteration i + 1 is looked up at iteration
+        // i (one scalar load in flight across an MFMA stream), and the V tile fetched at i + 1 is
+        // the K tile of i, whose row is known by then; tiles past the range read no table entry
+        auto tile_row = [&](int i) -> uint32_t {  // cache row of this group's i-th tile, or 0
+            const int kt = kt_lo + kKS * i + grp;
+            return i < n_mine && (kt + 1) * kKT <= T ? crow(kt * kKT) : 0u;
+        };
+        uint32_t row_k = 0, row_v = 0;
+        if constexpr (kPaged) {
+            row_k = tile_row(2);
+            row_v = tile_row(1);
+        }
         auto iter = [&](int i, floatx16& s, floatx16& sn) {
             const int tk = (kt_lo + kKS * (i + 2) + grp) * kKT, tv = (kt_lo + kKS * (i + 1) + grp) * kKT;
             const bool kdo = i + 2 < n_mine, vdo = i + 1 < n_mine;
             const bool kin = kdo && tk + kKT <= T, vin = vdo && tv + kKT <= T;
             if (kdo && !kin) dma_k(i + 2, i & 1);
             if (vdo && !vin) dma_v(i + 1, (i + 1) & 1);
-            const uint64_t sbk = kb_bytes + (uint64_t)(uint32_t)(tk + r0k) * row_bytes;
-            const uint64_t sbv = vb_bytes + (uint64_t)(uint32_t)(tv + 2 * i0v) * row_bytes;
+            const uint32_t rk = kPaged ? row_k : (uint32_t)tk, rv = kPaged ? row_v : (uint32_t)tv;
+            if constexpr (kPaged) {
+                row_v = row_k;
+                row_k = tile_row(i + 3);
+            }
+            const uint64_t sbk = kb_bytes + (uint64_t)(rk + r0k) * row_bytes;
+            const uint64_t sbv = vb_bytes + (uint64_t)(rv + 2 * i0v) * row_bytes;
             const uint32_t lbk = __builtin_amdgcn_readfirstlane(lds_addr(gsm + (i & 1) * kKTileF));
             const uint32_t lbv = __builtin_amdgcn_readfirstlane(lds_addr(gsv + ((i + 1) & 1) * kVTileF));
             if (i < n_mine)
@@ -630,9 +657,25 @@ size_t prefill_ws_bytes(int B, int H, int HKV, int max_kv) {
     return align256((size_t)k * rows * kHeadDim * sizeof(float)) + align256((size_t)k * rows * 2 * sizeof(float));
 }
 
+template <bool kNormQ, bool kPaged>
+static hipError_t launch_prefill_kernel(hipStream_t st, unsigned grid, size_t lds, const float* q, long q_stride,
+                                        float* out, const float* kc, const float* vc, const int* pos_dev, int B, int H,
+                                        int HKV, float scale, int ksplit, float* part_o, float* part_ml,
+                                        const float* q_gamma, const float* cs, float eps, const int* btab,
+                                        int bshift) {
+    static std::atomic<bool> opted;
+    if (const hipError_t e = opt_in_lds(opted, (const void*)k_prefill<kNormQ, kPaged>, lds); e != hipSuccess) return e;
+    k_prefill<kNormQ, kPaged><<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
+                                                                    ksplit, part_o, part_ml, q_gamma,
+                                                                    reinterpret_cast<const float2*>(cs), eps, btab,
+                                                                    bshift);
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
                           const float* vc, const int* pos_dev, int B, int H, int HKV, float scale, int ksplit,
-                          void* ws, const float* q_gamma, const float* cs, float eps) {
+                          void* ws, const float* q_gamma, const float* cs, float eps, const int* block_table,
+                          int block_shift) {
     if (ksplit < 1) ksplit = 1;
     const unsigned grid = (unsigned)prefill_grid1(B, H, HKV) * ksplit;
     float* part_o = nullptr;
@@ -645,17 +688,20 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
     const size_t lds = (size_t)kLdsF * sizeof(float);  // > 64 KB: opt in once
     static_assert(kQStageF == kVBaseF && kQStageF <= kLdsF, "merge exchange below the staging area");
     static_assert(kLdsF * sizeof(float) <= 160 * 1024, "LDS budget");
-    static std::atomic<bool> opted[2];
-    const bool nq = q_gamma != nullptr;
-    const void* f = nq ? (const void*)k_prefill<true> : (const void*)k_prefill<false>;
-    if (const hipError_t e = opt_in_lds(opted[nq], f, lds); e != hipSuccess) return e;
+    const bool nq = q_gamma != nullptr, pg = block_table != nullptr;
+    hipError_t e;
+    if (nq && pg) return hipErrorInvalidValue;  // not built: a paged step norms q in its prologue
     if (nq)
-        k_prefill<true><<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale, ksplit,
-                                                              part_o, part_ml, q_gamma,
-                                                              reinterpret_cast<const float2*>(cs), eps);
+        e = launch_prefill_kernel<true, false>(st, grid, lds, q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
+                                               ksplit, part_o, part_ml, q_gamma, cs, eps, nullptr, 0);
+    else if (pg)
+        e = launch_prefill_kernel<false, true>(st, grid, lds, q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
+                                               ksplit, part_o, part_ml, nullptr, nullptr, 0.f, block_table,
+                                               block_shift);
     else
-        k_prefill<false><<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
-                                                               ksplit, part_o, part_ml, nullptr, nullptr, 0.f);
+        e = launch_prefill_kernel<false, false>(st, grid, lds, q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
+                                                ksplit, part_o, part_ml, nullptr, nullptr, 0.f, nullptr, 0);
+    if (e != hipSuccess) return e;
     if (ksplit > 1) {
         const int rows = B * H;
         k_prefill_combine<<<(rows + 3) / 4, 128, 0, st>>>(part_o, part_ml, out, rows, ksplit);

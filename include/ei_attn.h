@@ -226,6 +226,22 @@ int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, float* out,
                     const float* k_gamma, const float* cs, int rope_dim, float eps, float scale, int max_kv, void* ws,
                     size_t ws_bytes);
 
+/* ei_prefill_step over a paged pool: key t of the sequence (its cache row before) is pool row
+ * block_table[t / block_size] * block_size + t % block_size, for the K and V pools kc and vc
+ * (rows of n_head_kv * 128 floats).  block_table is a device array of max_blocks int32 entries
+ * covering max_kv keys; block_size a power of two >= 32 (a 32-key prefill tile never straddles
+ * blocks).  The chunk's K/V rows are appended at the pool rows of positions *pos_dev ..
+ * *pos_dev + B - 1 (those blocks must be private to the sequence); blocks before may be shared
+ * with other sequences (a cached common prefix).  Results are bit-identical to ei_prefill_step on
+ * the same keys held contiguously.  No counterpart in the reference, which keeps one contiguous
+ * cache per sequence (src/cuda/model_cuda.cu:1571); it extends the paged decode
+ * (ei_decode_step_paged) to prompt chunks. */
+int ei_prefill_step_paged(ei_stream_t stream, float* qkv, long row_stride, float* out, float* kc, float* vc,
+                          const int* block_table, int max_blocks, int block_size, const int* pos_dev, int B,
+                          int n_head, int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma,
+                          const float* cs, int rope_dim, float eps, float scale, int max_kv, void* ws,
+                          size_t ws_bytes);
+
 /* ------------------------------------------------------------------ measurement
  * Not part of the reference path: the memory traffic of ei_attn_decode's plan for one sequence
  * of kv_len keys with no arithmetic (same grid, LDS-DMA instructions, tile order and cache
