@@ -37,21 +37,39 @@ def _kv(key: str, t: int, value) -> bytes:
     return out + struct.pack(fmt, value)
 
 
-def qwen3_tensors(model, f16: bool) -> list[tuple[str, np.ndarray]]:
-    """(GGUF name, array with ne[0] as its last axis) in file order; matrices F16 when f16."""
+def quantize_q8_0(a: np.ndarray) -> np.ndarray:
+    """Rows of a float matrix [rows][n] (n a multiple of 32) as Q8_0 blocks, uint8 [rows][n/32*34]:
+    per block of 32, d = max|x| / 127 stored as binary16 and q = round(x / d) in [-127, 127]."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    rows, n = a.shape
+    blk = a.reshape(rows, n // 32, 32)
+    d16 = (np.abs(blk).max(axis=2) / 127.0).astype(np.float16)
+    d = d16.astype(np.float32)
+    inv = np.where(d > 0, 1.0 / np.where(d > 0, d, 1.0), 0.0).astype(np.float32)
+    q = np.clip(np.rint(blk * inv[..., None]), -127, 127).astype(np.int8)
+    out = np.empty((rows, n // 32, 34), np.uint8)
+    out[..., :2] = d16.view(np.uint8).reshape(rows, n // 32, 2)
+    out[..., 2:] = q.view(np.uint8)
+    return out.reshape(rows, -1)
+
+
+def qwen3_tensors(model, f16: bool, q8_attn: bool = False) -> list[tuple[str, np.ndarray]]:
+    """(GGUF name, array with ne[0] as its last axis) in file order; matrices F16 when f16; the
+    attention projections Wq, Wk, Wv as Q8_0 blocks when q8_attn."""
     D = 128
     mat = (lambda a: np.ascontiguousarray(a, dtype=np.float16)) if f16 else (
         lambda a: np.ascontiguousarray(a, dtype=np.float32))
     vec = lambda a: np.ascontiguousarray(a, dtype=np.float32)
+    attn = (lambda a: Quantised(8, (a.shape[1], a.shape[0]), quantize_q8_0(a))) if q8_attn else mat
     QD, KD = model.H * D, model.HKV * D
     out = [("token_embd.weight", mat(model.emb)), ("output_norm.weight", vec(model.out_norm)),
            ("output.weight", mat(model.lm))]
     for l, L in enumerate(model.layers):
         b = f"blk.{l}."
         out += [(b + "attn_norm.weight", vec(L["attn_norm"])),
-                (b + "attn_q.weight", mat(L["wqkv"][:QD])),
-                (b + "attn_k.weight", mat(L["wqkv"][QD:QD + KD])),
-                (b + "attn_v.weight", mat(L["wqkv"][QD + KD:])),
+                (b + "attn_q.weight", attn(L["wqkv"][:QD])),
+                (b + "attn_k.weight", attn(L["wqkv"][QD:QD + KD])),
+                (b + "attn_v.weight", attn(L["wqkv"][QD + KD:])),
                 (b + "attn_q_norm.weight", vec(L["q_norm"])),
                 (b + "attn_k_norm.weight", vec(L["k_norm"])),
                 (b + "attn_output.weight", mat(L["wo"])),

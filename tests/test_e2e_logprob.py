@@ -152,3 +152,54 @@ def test_e2e_logprob_model_read_from_gguf(orc, gpu, tmp_path, f16):
     print(f"e2e from GGUF ({'F16' if f16 else 'F32'}): max |d logprob| = {d:.3e} over {len(ref)} positions",
           flush=True)
     assert d <= LOGPROB_TOL, f"max |delta logprob| {d:.2e} > {LOGPROB_TOL}"
+
+
+def _hip_projection(model, torch):
+    """project(l, x) on the GPU: ei_qkv_project on the file's own Wq, Wk, Wv bytes (one call per
+    segment and per four rows), the rows left raw for the attention step."""
+    from exactinfer_amd import _capi
+    from exactinfer_amd import attention as A
+    dev = "cuda"
+    segs = [[(ty, torch.from_numpy(np.ascontiguousarray(w).view(np.uint8)).to(dev), w.shape[0])
+             for ty, w in L["qkv_raw"]] for L in model.layers]
+    gam = [torch.from_numpy(L["attn_norm"]).to(dev) for L in model.layers]
+    width = (model.H + 2 * model.HKV) * HEAD_DIM
+
+    def project(l, x):
+        n, E = x.shape
+        xd = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(dev)
+        out = torch.empty((n, width), dtype=torch.float32, device=dev)
+        for r0 in range(0, n, 4):
+            rows, col = min(4, n - r0), 0
+            for ty, wd, nrows in segs[l]:
+                _capi.call("ei_qkv_project", A._stream(), xd[r0].data_ptr(), E, rows, E, gam[l].data_ptr(), 1e-6,
+                           wd.data_ptr(), ty, nrows, out[r0, col:].data_ptr(), width)
+                col += nrows
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    return project
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("weights", ["q8_0", "f16"])
+def test_e2e_logprob_gpu_projection_from_gguf(orc, gpu, tmp_path, weights):
+    """More of the layer on the GPU: the model read from a GGUF file (Wq, Wk, Wv as Q8_0 blocks or
+    F16), its attention RMSNorm + QKV projection through ei_qkv_project on the file's bytes, then
+    the HIP attention steps; against the reference's CPU chain on the same bytes (rmsnorm, matvec
+    of the stored weights, the reference attention).  The same |delta logprob| gate."""
+    import torch
+    from tests.golden.write_tiny_gguf import qwen3_metadata, qwen3_tensors, write_gguf
+    from tests.tiny_qwen3 import oracle_projection
+    src = TinyQwen3(seed=51, n_layer=2, n_embd=1024, n_head=8, n_head_kv=2, n_ff=512)
+    path = tmp_path / "tiny_proj.gguf"
+    write_gguf(path, qwen3_metadata(src), qwen3_tensors(src, weights == "f16", q8_attn=weights == "q8_0"))
+    model = TinyQwen3.from_gguf(path, dequant=orc.dequant)
+    toks = np.random.default_rng(52).integers(0, model.V, size=sum(CHUNKS) + N_DECODE + 1)
+    ref = run_sequence(model, oracle_attention(model, orc), toks, CHUNKS, N_DECODE, N_CTX,
+                       project=oracle_projection(model, orc))
+    hip = run_sequence(model, _hip_attention(model, gpu, torch), toks, CHUNKS, N_DECODE, N_CTX,
+                       project=_hip_projection(model, torch))
+    d = float(np.max(np.abs(hip - ref)))
+    print(f"e2e GPU projection ({weights}): max |d logprob| = {d:.3e} over {len(ref)} positions", flush=True)
+    assert d <= LOGPROB_TOL, f"max |delta logprob| {d:.2e} > {LOGPROB_TOL}"

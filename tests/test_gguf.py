@@ -242,3 +242,20 @@ def test_quantised_tensors_read_back(tmp_path, orc):
             got = g.tensor(name)
             assert got.dtype == np.uint8 and got.shape == want.shape and np.array_equal(got, want), name
             assert g.tensor_info(name)[0] == ty
+
+
+def test_q8_0_attention_weights_round_trip(tmp_path, orc):
+    """The writer's Q8_0 projections read back as the same blocks, and decode (the reference's
+    dequant) to within half a quantisation step of the weights they were made from."""
+    from exactinfer_amd.gguf import GgufFile
+    m = TinyQwen3(seed=61, n_layer=1, n_embd=256, n_head=4, n_head_kv=2)
+    p = _write(tmp_path, m, tensors=qwen3_tensors(m, False, q8_attn=True))
+    with GgufFile(p) as g:
+        blocks = g.tensor("blk.0.attn_q.weight")
+        assert g.tensor_info("blk.0.attn_q.weight")[0] == 8 and blocks.shape == (4 * 128, 256 // 32 * 34)
+    w = m.layers[0]["wqkv"][:4 * 128]
+    dq = orc.dequant(8, blocks, 256).reshape(w.shape)
+    d = np.abs(w).reshape(w.shape[0], -1, 32).max(axis=2) / 127.0
+    assert np.all(np.abs(dq - w).reshape(w.shape[0], -1, 32) <= 0.5 * d[..., None] * 1.01 + 1e-6)
+    model = TinyQwen3.from_gguf(p, dequant=orc.dequant)
+    assert np.array_equal(model.layers[0]["wqkv"][:4 * 128], dq)

@@ -61,10 +61,13 @@ class TinyQwen3:
         self.lm = mat(n_vocab, n_embd, gain=2.0)
 
     @classmethod
-    def from_gguf(cls, path) -> "TinyQwen3":
+    def from_gguf(cls, path, dequant=None) -> "TinyQwen3":
         """The model a GGUF file holds, read through this build's C++ reader (exactinfer_amd.gguf):
         configuration and tensor table validated as read_config / read_tensors do
-        (src/model.cpp:38-103); F16 matrices widened to float32 exactly."""
+        (src/model.cpp:38-103); F16 matrices widened to float32 exactly.  Quantised tensors are
+        decoded with dequant(type, blocks, n) (the oracle's decode of the reference's formats), and
+        the attention projections also keep their raw bytes (layer key "qkv_raw": (type, blocks)
+        of Wq, Wk, Wv) for a projection that reads the blocks themselves."""
         from exactinfer_amd.gguf import GgufFile
         self = cls.__new__(cls)
         D = HEAD_DIM
@@ -72,7 +75,20 @@ class TinyQwen3:
             c = g.qwen3_config()
             if c["head_dim"] != D or c["rope_dim"] != D:
                 raise ValueError("the harness is built for head_dim = rope_dim = 128")
-            t = lambda n: np.ascontiguousarray(g.tensor(n), dtype=np.float32)
+
+            def t(n):
+                a = g.tensor(n)
+                ty, ne, _ = g.tensor_info(n)
+                if ty in (0, 1):
+                    return np.ascontiguousarray(a, dtype=np.float32)
+                if dequant is None:
+                    raise ValueError(f"{n}: quantised (type {ty}) and no dequant given")
+                return dequant(ty, a, ne[0]).reshape(a.shape[0], ne[0])
+
+            def raw(n):
+                ty = g.tensor_info(n)[0]
+                a = g.tensor(n)
+                return ty, (a.view(np.uint16) if ty == 1 else np.ascontiguousarray(a))
             self.n_layer, self.E, self.H, self.HKV, self.V = (c["n_layer"], c["n_embd"], c["n_head"], c["n_head_kv"],
                                                               c["n_vocab"])
             self.emb = t("token_embd.weight")
@@ -84,6 +100,7 @@ class TinyQwen3:
                 self.layers.append(dict(
                     attn_norm=t(b + "attn_norm.weight"),
                     wqkv=np.concatenate([t(b + "attn_q.weight"), t(b + "attn_k.weight"), t(b + "attn_v.weight")]),
+                    qkv_raw=[raw(b + "attn_q.weight"), raw(b + "attn_k.weight"), raw(b + "attn_v.weight")],
                     q_norm=t(b + "attn_q_norm.weight"), k_norm=t(b + "attn_k_norm.weight"),
                     wo=t(b + "attn_output.weight"), ffn_norm=t(b + "ffn_norm.weight"),
                     wg=t(b + "ffn_gate.weight"), wu=t(b + "ffn_up.weight"), wd=t(b + "ffn_down.weight")))
@@ -93,12 +110,16 @@ class TinyQwen3:
     def qkv_width(self) -> int:
         return (self.H + 2 * self.HKV) * HEAD_DIM
 
-    def forward(self, tokens: np.ndarray, pos0: int, attn) -> np.ndarray:
-        """Logits [n, vocab] for tokens at positions pos0.. ; attn(l, qkv [n, qkv_width], pos0) -> [n, H*128]."""
+    def forward(self, tokens: np.ndarray, pos0: int, attn, project=None) -> np.ndarray:
+        """Logits [n, vocab] for tokens at positions pos0.. ; attn(l, qkv [n, qkv_width], pos0) -> [n, H*128].
+        project(l, x) -> qkv [n, qkv_width], when given, replaces the attention RMSNorm + QKV product."""
         x = self.emb[tokens]
         for l, L in enumerate(self.layers):
-            h = _rmsnorm(x, L["attn_norm"])
-            qkv = np.ascontiguousarray(h @ L["wqkv"].T, dtype=np.float32)
+            if project is not None:
+                qkv = np.ascontiguousarray(project(l, x), dtype=np.float32)
+            else:
+                h = _rmsnorm(x, L["attn_norm"])
+                qkv = np.ascontiguousarray(h @ L["wqkv"].T, dtype=np.float32)
             att = attn(l, qkv, pos0)
             x = x + att @ L["wo"].T
             h = _rmsnorm(x, L["ffn_norm"])
@@ -115,7 +136,7 @@ def logprobs(logits: np.ndarray, targets: np.ndarray) -> np.ndarray:
 
 
 def run_sequence(model: TinyQwen3, attn_factory, tokens: np.ndarray, chunks: list[int], n_decode: int,
-                 n_ctx: int) -> np.ndarray:
+                 n_ctx: int, project=None) -> np.ndarray:
     """Prompt in `chunks` (prefill), then `n_decode` greedy-free decode steps on the given tokens.
 
     `tokens` holds sum(chunks) + n_decode + 1 ids; the logprob of token i+1 is scored at every
@@ -125,11 +146,11 @@ def run_sequence(model: TinyQwen3, attn_factory, tokens: np.ndarray, chunks: lis
     out = []
     pos = 0
     for n in chunks:
-        lg = model.forward(tokens[pos:pos + n], pos, attn)
+        lg = model.forward(tokens[pos:pos + n], pos, attn, project)
         out.append(logprobs(lg, tokens[pos + 1:pos + n + 1]))
         pos += n
     for _ in range(n_decode):
-        lg = model.forward(tokens[pos:pos + 1], pos, attn)
+        lg = model.forward(tokens[pos:pos + 1], pos, attn, project)
         out.append(logprobs(lg, tokens[pos + 1:pos + 2]))
         pos += 1
     return np.concatenate(out)
@@ -203,3 +224,17 @@ class PrefixServer:
         toks, lps = greedy_generate(self.model, self.attn, prompt, n, self.chunk, start)
         self.cached = [int(t) for t in prompt] + toks[:-1]  # the last generated token is not evaluated
         return toks, lps, start
+
+
+def oracle_projection(model: TinyQwen3, O):
+    """project(l, x) of the reference's CPU path on the file's own weights: rmsnorm
+    (src/ops.cpp:155-160), then matvec of Wq, Wk, Wv as stored (dot_f32 / dot_f16, or the
+    quantised decode + dot_f32; src/ops.cpp:126-153)."""
+    def project(l, x):
+        L = model.layers[l]
+        rows = []
+        for b in range(x.shape[0]):
+            h = O.rmsnorm(np.ascontiguousarray(x[b], dtype=np.float32), L["attn_norm"])
+            rows.append(np.concatenate([O.matvec(w, h, ty) for ty, w in L["qkv_raw"]]))
+        return np.stack(rows)
+    return project
