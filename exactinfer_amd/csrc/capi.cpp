@@ -416,7 +416,7 @@ namespace {
 int prefill_step_impl(ei_stream_t stream, float* qkv, long row_stride, float* out, float* kc, float* vc,
                       const int* pos_dev, int B, int n_head, int n_head_kv, int head_dim, const float* q_gamma,
                       const float* k_gamma, const float* cs, int rope_dim, float eps, float scale, int max_kv, void* ws,
-                      size_t ws_bytes, const int* block_table, int block_shift) {
+                      size_t ws_bytes, const int* block_table, int block_shift, int max_blocks) {
     if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
     if (int e = check_rope(rope_dim, head_dim)) return e;
     REQUIRE(qkv && out && kc && vc && pos_dev && q_gamma && k_gamma && cs, "null pointer argument");
@@ -441,11 +441,11 @@ int prefill_step_impl(ei_stream_t stream, float* qkv, long row_stride, float* ou
     const bool fuse_q = rope_dim == head_dim && ksplit <= 2 && block_table == nullptr;
     if (int e = hip_status(ei::launch_qkv_prepare(st, qkv, B, row_stride, n_head, n_head_kv, q_gamma, k_gamma, cs,
                                                   pos_dev, rope_dim, eps, kc, vc, fuse_q ? n_head : 0, block_table,
-                                                  block_shift),
+                                                  block_shift, max_blocks),
                            "prefill step: prologue launch"))
         return e;
     return hip_status(ei::launch_prefill(st, qkv, row_stride, out, kc, vc, pos_dev, B, n_head, n_head_kv, scale, ksplit,
-                                         ws, fuse_q ? q_gamma : nullptr, cs, eps, block_table, block_shift),
+                                         ws, fuse_q ? q_gamma : nullptr, cs, eps, block_table, block_shift, max_blocks),
                       "prefill step: attention launch");
 }
 
@@ -456,7 +456,7 @@ EI_API int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, floa
                            const float* k_gamma, const float* cs, int rope_dim, float eps, float scale, int max_kv,
                            void* ws, size_t ws_bytes) {
     return prefill_step_impl(stream, qkv, row_stride, out, kc, vc, pos_dev, B, n_head, n_head_kv, head_dim, q_gamma,
-                             k_gamma, cs, rope_dim, eps, scale, max_kv, ws, ws_bytes, nullptr, 0);
+                             k_gamma, cs, rope_dim, eps, scale, max_kv, ws, ws_bytes, nullptr, 0, 0);
 }
 
 EI_API int ei_prefill_step_paged(ei_stream_t stream, float* qkv, long row_stride, float* out, float* kc, float* vc,
@@ -472,7 +472,7 @@ EI_API int ei_prefill_step_paged(ei_stream_t stream, float* qkv, long row_stride
     int shift = 0;
     while ((1 << shift) < block_size) ++shift;
     return prefill_step_impl(stream, qkv, row_stride, out, kc, vc, pos_dev, B, n_head, n_head_kv, head_dim, q_gamma,
-                             k_gamma, cs, rope_dim, eps, scale, max_kv, ws, ws_bytes, block_table, shift);
+                             k_gamma, cs, rope_dim, eps, scale, max_kv, ws, ws_bytes, block_table, shift, max_blocks);
 }
 
 EI_API int ei_qkv_project(ei_stream_t stream, const float* x, long x_stride, int rows, int n_embd,

@@ -312,12 +312,15 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     // this split's record line (its (m, l) per head slot; word 1: the XCD it ran on)
     uint32_t* unit_rec = a.rec + (size_t)unit * S * kRec;
     uint32_t* my_rec = unit_rec + split * kRec;
-    const int len = a.kv_len ? a.kv_len[seq] : (*a.pos_dev + 1);
+    const int len_in = a.kv_len ? a.kv_len[seq] : (*a.pos_dev + 1);
     const size_t KD = (size_t)a.HKV * D;
     const size_t row0 = a.kv_offset ? (size_t)a.kv_offset[seq] : 0;
     // cache row of this sequence's key t: contiguous from row0, or through the block table
     const int* btab = a.block_table ? a.block_table + (size_t)seq * a.max_blocks : nullptr;
     const int bshift = a.block_shift, bmask = (1 << bshift) - 1;
+    // paged: keys past the table's blocks (a length outside the contract) are neither read nor
+    // appended, so no table entry beyond max_blocks is ever loaded
+    const int len = btab ? min(len_in, a.max_blocks << bshift) : len_in;
     auto phys = [&](int t) -> size_t {
         return btab ? ((size_t)btab[t >> bshift] << bshift) | (size_t)(t & bmask) : (size_t)t;
     };
@@ -327,7 +330,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     // the last split takes every key past the plan (a kv_len above the planned max_kv is
     // still attended in full, and the fused step still finds the new row's owner)
     const int t_end = split == S - 1 ? len : min(len, t_begin + a.chunk);
-    const int pos = len > 0 ? len - 1 : 0;  // a zero-length sequence has no new row; keep the table index valid
+    const int pos = len_in > 0 ? len_in - 1 : 0;  // a zero-length sequence has no new row; keep the table index valid
     const float* qrow = a.q + (size_t)seq * a.q_stride;
     const int Gr = a.H / a.HKV;  // heads of this KV head (<= G; heads Gr..G-1 are padding)
     const int h0 = kvh * Gr;
@@ -359,7 +362,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
         return (size_t)(uint32_t)(i < 64 ? __builtin_amdgcn_readlane(lane_row, i)
                                          : __builtin_amdgcn_readlane(lane_row2, i - 64));
     };
-    const bool owner = FUSED && t_begin <= pos && pos < t_end;
+    const bool owner = FUSED && t_begin <= pos && pos < t_end;  // pos >= t_end when len was capped
     const size_t pos_row = owner ? phys(pos) : 0;  // read before any DMA is in flight
     // The waves' DMA issue is back-pressured by the CU's request queue, so a wave spends most
     // of the stream waiting to get its instructions accepted.  Nothing waits at a workgroup

@@ -47,7 +47,7 @@ hipError_t launch_kv_append(hipStream_t st, const float* k_src, const float* v_s
 hipError_t launch_qkv_prepare(hipStream_t st, float* qkv, int rows, long row_stride, int H, int HKV,
                               const float* q_gamma, const float* k_gamma, const float* cs, const int* pos_dev,
                               int rope_dim, float eps, float* kc, float* vc, int h_begin = 0,
-                              const int* block_table = nullptr, int block_shift = 0);
+                              const int* block_table = nullptr, int block_shift = 0, int max_blocks = 0);
 hipError_t launch_synth_fill(hipStream_t st, float* dst, size_t n, uint64_t seed, uint64_t offset, long row_len,
                              long spike_every, float spike_mult);
 
@@ -133,6 +133,6 @@ size_t prefill_ws_bytes(int B, int H, int HKV, int max_kv);  // 0 when no split 
 hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
                           const float* vc, const int* pos_dev, int B, int H, int HKV, float scale, int ksplit,
                           void* ws, const float* q_gamma = nullptr, const float* cs = nullptr, float eps = 0.f,
-                          const int* block_table = nullptr, int block_shift = 0);
+                          const int* block_table = nullptr, int block_shift = 0, int max_blocks = 0);
 
 }  // namespace ei

@@ -157,7 +157,8 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
                                                            float* __restrict__ part_o, float* __restrict__ part_ml,
                                                            const float* __restrict__ q_gamma,
                                                            const float2* __restrict__ cs, float eps,
-                                                           const int* __restrict__ btab, int bshift) {
+                                                           const int* __restrict__ btab, int bshift,
+                                                           int max_blocks) {
     constexpr int D = kHeadDim;
     constexpr int GW = kSlots;
     constexpr int DMA_PER_WAVE = 16 / GW;  // V DMA instructions per wave per tile (K: twice as many, 32 lanes each)
@@ -182,7 +183,9 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
     const uint32_t row_bytes = (uint32_t)(KD * sizeof(float));          // one cache row (all KV heads)
     // cache row of key t (wave-uniform t: one scalar load of the block table when paged)
     auto crow = [&](int t) -> uint32_t {
-        if constexpr (kPaged) return ((uint32_t)btab[t >> bshift] << bshift) | ((uint32_t)t & ((1u << bshift) - 1u));
+        // (a key past the table's blocks, outside the contract, reads the last entry: no fault)
+        if constexpr (kPaged)
+            return ((uint32_t)btab[min(t >> bshift, max_blocks - 1)] << bshift) | ((uint32_t)t & ((1u << bshift) - 1u));
         else return (uint32_t)t;
     };
     const uint32_t voff_k = 16u * col;                                  // K: lanes 0..31, one row
@@ -662,20 +665,20 @@ static hipError_t launch_prefill_kernel(hipStream_t st, unsigned grid, size_t ld
                                         float* out, const float* kc, const float* vc, const int* pos_dev, int B, int H,
                                         int HKV, float scale, int ksplit, float* part_o, float* part_ml,
                                         const float* q_gamma, const float* cs, float eps, const int* btab,
-                                        int bshift) {
+                                        int bshift, int max_blocks) {
     static std::atomic<bool> opted;
     if (const hipError_t e = opt_in_lds(opted, (const void*)k_prefill<kNormQ, kPaged>, lds); e != hipSuccess) return e;
     k_prefill<kNormQ, kPaged><<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
                                                                     ksplit, part_o, part_ml, q_gamma,
                                                                     reinterpret_cast<const float2*>(cs), eps, btab,
-                                                                    bshift);
+                                                                    bshift, max_blocks);
     return hipGetLastError();
 }
 
 hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* out, const float* kc,
                           const float* vc, const int* pos_dev, int B, int H, int HKV, float scale, int ksplit,
                           void* ws, const float* q_gamma, const float* cs, float eps, const int* block_table,
-                          int block_shift) {
+                          int block_shift, int max_blocks) {
     if (ksplit < 1) ksplit = 1;
     const unsigned grid = (unsigned)prefill_grid1(B, H, HKV) * ksplit;
     float* part_o = nullptr;
@@ -693,14 +696,14 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
     if (nq && pg) return hipErrorInvalidValue;  // not built: a paged step norms q in its prologue
     if (nq)
         e = launch_prefill_kernel<true, false>(st, grid, lds, q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
-                                               ksplit, part_o, part_ml, q_gamma, cs, eps, nullptr, 0);
+                                               ksplit, part_o, part_ml, q_gamma, cs, eps, nullptr, 0, 0);
     else if (pg)
         e = launch_prefill_kernel<false, true>(st, grid, lds, q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
                                                ksplit, part_o, part_ml, nullptr, nullptr, 0.f, block_table,
-                                               block_shift);
+                                               block_shift, max_blocks);
     else
         e = launch_prefill_kernel<false, false>(st, grid, lds, q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
-                                                ksplit, part_o, part_ml, nullptr, nullptr, 0.f, nullptr, 0);
+                                                ksplit, part_o, part_ml, nullptr, nullptr, 0.f, nullptr, 0, 0);
     if (e != hipSuccess) return e;
     if (ksplit > 1) {
         const int rows = B * H;

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void k_qkv_prepare(float* __restrict__ qkv, lo
                                                      const float2* __restrict__ cs, const int* __restrict__ pos_dev,
                                                      int rope_dim, float eps, float* __restrict__ kc,
                                                      float* __restrict__ vc, int h_begin,
-                                                     const int* __restrict__ btab, int bshift) {
+                                                     const int* __restrict__ btab, int bshift, int max_blocks) {
     __shared__ float scratch[4][kHeadDim];
     const int b = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int NH = H + HKV;
@@ -87,7 +87,8 @@ __global__ __launch_bounds__(256) void k_qkv_prepare(float* __restrict__ qkv, lo
         float* v = row + (size_t)hh * kHeadDim;
         v[lane] = o0;
         v[lane + 64] = o1;
-        if (is_k) {
+        // (paged: a position past the table's blocks, outside the contract, appends nothing)
+        if (is_k && (!btab || (pos >> bshift) < max_blocks)) {
             const int kvh = hh - H;
             // cache row of the position: itself, or through the block table of a paged pool
             const size_t crow = btab ? ((size_t)btab[pos >> bshift] << bshift) | (size_t)(pos & ((1 << bshift) - 1))
@@ -131,17 +132,17 @@ hipError_t launch_kv_append(hipStream_t st, const float* k_src, const float* v_s
 hipError_t launch_qkv_prepare(hipStream_t st, float* qkv, int rows, long row_stride, int H, int HKV,
                               const float* q_gamma, const float* k_gamma, const float* cs, const int* pos_dev,
                               int rope_dim, float eps, float* kc, float* vc, int h_begin, const int* block_table,
-                              int block_shift) {
+                              int block_shift, int max_blocks) {
     const int nh = H + HKV - h_begin;
     const float2* cs2 = reinterpret_cast<const float2*>(cs);
     if (nh <= 8) {  // 4 waves x 2 heads
         k_qkv_prepare<2><<<dim3(rows, (nh + 7) / 8), 256, 0, st>>>(qkv, row_stride, H, HKV, q_gamma, k_gamma, cs2,
                                                                      pos_dev, rope_dim, eps, kc, vc, h_begin,
-                                                                     block_table, block_shift);
+                                                                     block_table, block_shift, max_blocks);
     } else {  // 4 waves x 4 heads
         k_qkv_prepare<4><<<dim3(rows, (nh + 15) / 16), 256, 0, st>>>(qkv, row_stride, H, HKV, q_gamma, k_gamma, cs2,
                                                                        pos_dev, rope_dim, eps, kc, vc, h_begin,
-                                                                     block_table, block_shift);
+                                                                     block_table, block_shift, max_blocks);
     }
     return hipGetLastError();
 }

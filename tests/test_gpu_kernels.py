@@ -541,3 +541,45 @@ def test_decode_step_paged_appends_to_physical_rows(orc, gpu):
         vv = _gather(rv.reshape(n_rows, HKV, D), table, s, n, bs)
         ref = orc.attn_decode(normed[s][0, :H * D].reshape(H, D), kk, vv, int(n), H, HKV, D)
         assert rel_err(out[s], ref) <= ATTN_RTOL, f"sequence {s}"
+
+
+def test_decode_step_paged_length_past_table(orc, gpu):
+    """A kv_len longer than the table covers (max_blocks x block_size, outside the contract):
+    the kernel reads no table entry past max_blocks.  That sequence attends over the keys its
+    table holds, with q at the position its length names, and appends nothing; the other
+    sequences of the batch are unaffected."""
+    H, HKV, bs = 16, 8, 32
+    rng = np.random.default_rng(42)
+    lens = np.array([96, 200, 45], np.int32)  # in-table lengths; sequence 0 is then made longer
+    table, nblocks = _paged_layout(rng, lens, bs, 0)
+    cap = table.shape[1] * bs  # 224: sequence 0's 3 blocks are padded to the widest table with block 0
+    table[0, 3:] = table[0, 0]
+    lens[0] = cap + 9
+    n_rows = nblocks * bs
+    pool_k, pool_v = _cache(orc, n_rows, HKV, 4200)
+    qkv = orc.normal((len(lens), (H + 2 * HKV) * D), 4201)
+    qg, kg = orc.gamma(D, 7), orc.gamma(D, 8)
+    cs = gpu.rope_table(int(lens.max()))
+    shape = gpu.AttnShape(H, HKV)
+    ws = gpu.DecodeWorkspace(len(lens), H, HKV, max_kv=cap)  # the host accepts a plan the table covers
+    kd, vd = _dev(pool_k), _dev(pool_v)
+    out = _host(gpu.decode_step_paged(_dev(qkv), kd, vd, _dev(table), bs, _dev(lens), shape, _dev(qg), _dev(kg), cs,
+                                      ws))
+    rk, rv = pool_k.reshape(n_rows, -1).copy(), pool_v.reshape(n_rows, -1).copy()
+    normed = []
+    for s, n in enumerate(lens):
+        pos = int(n) - 1
+        row = orc.headnorm_rope(qkv[s:s + 1], H, D, qg, pos, 128, 1e6, 1e-6)
+        row = orc.headnorm_rope(row, HKV, D, kg, pos, 128, 1e6, 1e-6, col0=H * D)
+        if s > 0:
+            phys = table[s, pos // bs] * bs + pos % bs
+            rk[phys] = row[0, H * D:(H + HKV) * D]
+            rv[phys] = row[0, (H + HKV) * D:]
+        normed.append(row)
+    assert bits_equal(_host(kd).reshape(n_rows, -1), rk) and bits_equal(_host(vd).reshape(n_rows, -1), rv)
+    for s, n in enumerate(lens):
+        n = min(int(n), cap)
+        kk = _gather(rk.reshape(n_rows, HKV, D), table, s, n, bs)
+        vv = _gather(rv.reshape(n_rows, HKV, D), table, s, n, bs)
+        ref = orc.attn_decode(normed[s][0, :H * D].reshape(H, D), kk, vv, n, H, HKV, D)
+        assert rel_err(out[s], ref) <= ATTN_RTOL, f"sequence {s}"
