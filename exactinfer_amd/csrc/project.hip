@@ -202,13 +202,17 @@ __device__ __forceinline__ void decode16(const uint8_t* row, int k, float* wv) {
     if constexpr (T == 8) {  // Q8_0: y = q * d (src/quant.cpp:7-13)
         const uint8_t* blk = row + 34 * (k >> 1);
         const float d = f16_bits(lds_u16(blk));
+        const float off = -128.f * d;  // exact (a power-of-two scaling)
         const u32x4_t q = lds_16bytes(blk + 2 + 16 * (k & 1));
         const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t u = qw[i] ^ 0x80808080u;  // int8 q + 128 per byte
+            // (q + 128) d - 128 d in one rounding: the exact value is q d, so this is the
+            // correctly rounded q * d the reference computes (a zero comes out +0 where the
+            // reference may have -0, which changes no sum but an exact zero's sign)
 #pragma unroll
-            for (int b = 0; b < 4; ++b) wv[4 * i + b] = (ubyte_f(u, b) - 128.f) * d;
+            for (int b = 0; b < 4; ++b) wv[4 * i + b] = __builtin_fmaf(ubyte_f(u, b), d, off);
         }
     } else if constexpr (T == 12) {  // Q4_K: y = (d sc) q - dmin m (src/quant.cpp:15-33)
         const uint8_t* blk = row + 144 * (k >> 4);
@@ -242,6 +246,8 @@ __device__ __forceinline__ void decode16(const uint8_t* row, int k, float* wv) {
         const int v = (k & 15) * 16, h = v >> 7, g = (v >> 5) & 3, l = v & 31;
         const float d = f16_bits(lds_u16(blk + 208));
         const float dsc = d * (float)(int8_t)blk[192 + 8 * h + (l >> 4) + 2 * g];
+        // dsc q - 32 dsc in one rounding (32 dsc is exact): the correctly rounded dsc (q - 32)
+        const float off = -32.f * dsc;
         const u32x4_t ql = lds_16bytes(blk + 64 * h + l + 32 * (g & 1));
         const u32x4_t qh = lds_16bytes(blk + 128 + 32 * h + l);
         const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w}, hw[4] = {qh.x, qh.y, qh.z, qh.w};
@@ -250,7 +256,7 @@ __device__ __forceinline__ void decode16(const uint8_t* row, int k, float* wv) {
             const uint32_t lo = (lw[i] >> (4 * (g >> 1))) & 0x0F0F0F0Fu;
             const uint32_t q6 = lo | (((hw[i] >> (2 * g)) & 0x03030303u) << 4);  // 0..63 per byte
 #pragma unroll
-            for (int b = 0; b < 4; ++b) wv[4 * i + b] = dsc * (ubyte_f(q6, b) - 32.f);
+            for (int b = 0; b < 4; ++b) wv[4 * i + b] = __builtin_fmaf(dsc, ubyte_f(q6, b), off);
         }
     }
 }
