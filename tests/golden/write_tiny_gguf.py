@@ -53,14 +53,104 @@ def quantize_q8_0(a: np.ndarray) -> np.ndarray:
     return out.reshape(rows, -1)
 
 
-def qwen3_tensors(model, f16: bool, q8_attn: bool = False) -> list[tuple[str, np.ndarray]]:
+def _f16_bytes(v: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(v, dtype=np.float16).view(np.uint8).reshape(*v.shape, 2)
+
+
+def quantize_q4_k(a: np.ndarray) -> np.ndarray:
+    """Rows [rows][n] (n a multiple of 256) as Q4_K blocks, uint8 [rows][n/256*144].  A plain
+    encoder (not llama.cpp's search): sub-block j of 32 values gets y = dl_j q - ml_j with
+    ml_j = -min(0, min x) and dl_j = (max x + ml_j) / 15; dl_j and ml_j are 6-bit multiples of
+    the block's d and dmin (binary16), q = round((x + ml) / dl) in 0..15.  Layout as the decoder
+    reads it (src/quant.cpp:15-33, the scale packing of src/quant.h:43-52): d, dmin, 12 packed
+    scale bytes, then 4 chunks of 32 bytes whose low nibbles hold sub-block 2c, high 2c+1."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    rows, n = a.shape
+    nb = rows * (n // 256)
+    x = a.reshape(nb, 8, 32)
+    ml = -np.minimum(x.min(axis=2), 0.0)
+    dl = (x.max(axis=2) + ml) / 15.0
+    d16 = (dl.max(axis=1) / 63.0).astype(np.float16)
+    m16 = (ml.max(axis=1) / 63.0).astype(np.float16)
+    d, dm = d16.astype(np.float32), m16.astype(np.float32)
+    safe = lambda v: np.where(v > 0, v, 1.0)
+    sc = np.where(d[:, None] > 0, np.clip(np.rint(dl / safe(d)[:, None]), 0, 63), 0).astype(np.int32)
+    mq = np.where(dm[:, None] > 0, np.clip(np.rint(ml / safe(dm)[:, None]), 0, 63), 0).astype(np.int32)
+    dle = d[:, None] * sc.astype(np.float32)
+    mle = dm[:, None] * mq.astype(np.float32)
+    q = np.where(dle[..., None] > 0, np.rint((x + mle[..., None]) / safe(dle)[..., None]), 0)
+    q = np.clip(q, 0, 15).astype(np.uint8)
+    out = np.zeros((nb, 144), np.uint8)
+    out[:, 0:2] = _f16_bytes(d16)
+    out[:, 2:4] = _f16_bytes(m16)
+    scb = np.zeros((nb, 12), np.int32)
+    for j in range(4):
+        scb[:, j] = (sc[:, j] & 63) | ((sc[:, j + 4] >> 4) << 6)
+        scb[:, j + 4] = (mq[:, j] & 63) | ((mq[:, j + 4] >> 4) << 6)
+        scb[:, j + 8] = (sc[:, j + 4] & 15) | ((mq[:, j + 4] & 15) << 4)
+    out[:, 4:16] = scb.astype(np.uint8)
+    for c in range(4):
+        out[:, 16 + 32 * c:48 + 32 * c] = q[:, 2 * c] | (q[:, 2 * c + 1] << 4)
+    return out.reshape(rows, -1)
+
+
+def quantize_q6_k(a: np.ndarray) -> np.ndarray:
+    """Rows [rows][n] (n a multiple of 256) as Q6_K blocks, uint8 [rows][n/256*210].  A plain
+    encoder: each group of 16 values gets y = d sc (q - 32) with sc an int8 multiple of the
+    block's d (binary16) and q = round(x / (d sc)) + 32 in 0..63.  Layout as the decoder reads
+    it (src/quant.cpp:35-60): value v of half h = v / 128, g = (v / 32) % 4, l = v % 32 keeps
+    its low 4 bits in ql[64 h + 32 (g % 2) + l] (high nibble when g >= 2), its top 2 bits in
+    qh[32 h + l] at bit 2 g, and its scale in scales[8 h + 2 g + l / 16]."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    rows, n = a.shape
+    nb = rows * (n // 256)
+    x = a.reshape(nb, 256)
+    v = np.arange(256)
+    h, g, l = v // 128, (v // 32) % 4, v % 32
+    sidx = 8 * h + 2 * g + l // 16  # scale index of every value
+    amax = np.zeros((nb, 16), np.float32)
+    for i in range(16):
+        amax[:, i] = np.abs(x[:, sidx == i]).max(axis=1)
+    s = amax / 31.0
+    d16 = (s.max(axis=1) / 127.0).astype(np.float16)
+    d = d16.astype(np.float32)
+    safe = lambda t: np.where(t > 0, t, 1.0)
+    sc = np.where(d[:, None] > 0, np.clip(np.rint(s / safe(d)[:, None]), 0, 127), 0).astype(np.int32)
+    step = (d[:, None] * sc.astype(np.float32))[:, sidx]
+    q = np.where(step > 0, np.rint(x / safe(step)), 0)
+    q = (np.clip(q, -32, 31) + 32).astype(np.int32)
+    out = np.zeros((nb, 210), np.uint8)
+    ql = np.zeros((nb, 128), np.int32)
+    qh = np.zeros((nb, 64), np.int32)
+    for vi in range(256):
+        hh, gg, ll = int(h[vi]), int(g[vi]), int(l[vi])
+        ql[:, 64 * hh + 32 * (gg & 1) + ll] |= (q[:, vi] & 15) << (4 * (gg >> 1))
+        qh[:, 32 * hh + ll] |= (q[:, vi] >> 4) << (2 * gg)
+    out[:, 0:128] = ql.astype(np.uint8)
+    out[:, 128:192] = qh.astype(np.uint8)
+    out[:, 192:208] = sc.astype(np.int8).view(np.uint8)
+    out[:, 208:210] = _f16_bytes(d16)
+    return out.reshape(rows, -1)
+
+
+QUANTIZERS = {"q8_0": (8, quantize_q8_0), "q4_k": (12, quantize_q4_k), "q6_k": (14, quantize_q6_k)}
+
+
+def qwen3_tensors(model, f16: bool, q8_attn: bool = False, attn_type: str | None = None) -> list[tuple[str, np.ndarray]]:
     """(GGUF name, array with ne[0] as its last axis) in file order; matrices F16 when f16; the
-    attention projections Wq, Wk, Wv as Q8_0 blocks when q8_attn."""
+    attention projections Wq, Wk, Wv as blocks of attn_type ("q8_0", "q4_k", "q6_k"; q8_attn is
+    attn_type "q8_0")."""
     D = 128
     mat = (lambda a: np.ascontiguousarray(a, dtype=np.float16)) if f16 else (
         lambda a: np.ascontiguousarray(a, dtype=np.float32))
     vec = lambda a: np.ascontiguousarray(a, dtype=np.float32)
-    attn = (lambda a: Quantised(8, (a.shape[1], a.shape[0]), quantize_q8_0(a))) if q8_attn else mat
+    if q8_attn:
+        attn_type = "q8_0"
+    if attn_type:
+        tid, quant = QUANTIZERS[attn_type]
+        attn = lambda a: Quantised(tid, (a.shape[1], a.shape[0]), quant(a))
+    else:
+        attn = mat
     QD, KD = model.H * D, model.HKV * D
     out = [("token_embd.weight", mat(model.emb)), ("output_norm.weight", vec(model.out_norm)),
            ("output.weight", mat(model.lm))]

@@ -182,10 +182,10 @@ def _hip_projection(model, torch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("weights", ["q8_0", "f16"])
+@pytest.mark.parametrize("weights", ["q8_0", "q4_k", "q6_k", "f16"])
 def test_e2e_logprob_gpu_projection_from_gguf(orc, gpu, tmp_path, weights):
-    """More of the layer on the GPU: the model read from a GGUF file (Wq, Wk, Wv as Q8_0 blocks or
-    F16), its attention RMSNorm + QKV projection through ei_qkv_project on the file's bytes, then
+    """More of the layer on the GPU: the model read from a GGUF file (Wq, Wk, Wv as Q8_0, Q4_K or
+    Q6_K blocks, or F16), its attention RMSNorm + QKV projection through ei_qkv_project on the file's bytes, then
     the HIP attention steps; against the reference's CPU chain on the same bytes (rmsnorm, matvec
     of the stored weights, the reference attention).  The same |delta logprob| gate."""
     import torch
@@ -193,7 +193,8 @@ def test_e2e_logprob_gpu_projection_from_gguf(orc, gpu, tmp_path, weights):
     from tests.tiny_qwen3 import oracle_projection
     src = TinyQwen3(seed=51, n_layer=2, n_embd=1024, n_head=8, n_head_kv=2, n_ff=512)
     path = tmp_path / "tiny_proj.gguf"
-    write_gguf(path, qwen3_metadata(src), qwen3_tensors(src, weights == "f16", q8_attn=weights == "q8_0"))
+    write_gguf(path, qwen3_metadata(src), qwen3_tensors(src, weights == "f16",
+                                                                 attn_type=None if weights == "f16" else weights))
     model = TinyQwen3.from_gguf(path, dequant=orc.dequant)
     toks = np.random.default_rng(52).integers(0, model.V, size=sum(CHUNKS) + N_DECODE + 1)
     ref = run_sequence(model, oracle_attention(model, orc), toks, CHUNKS, N_DECODE, N_CTX,

@@ -259,3 +259,26 @@ def test_q8_0_attention_weights_round_trip(tmp_path, orc):
     assert np.all(np.abs(dq - w).reshape(w.shape[0], -1, 32) <= 0.5 * d[..., None] * 1.01 + 1e-6)
     model = TinyQwen3.from_gguf(p, dequant=orc.dequant)
     assert np.array_equal(model.layers[0]["wqkv"][:4 * 128], dq)
+
+
+@pytest.mark.parametrize("attn_type,tid,rel_bound", [("q4_k", 12, 0.08), ("q6_k", 14, 0.025)])
+def test_k_quant_attention_weights_round_trip(tmp_path, orc, attn_type, tid, rel_bound):
+    """The writer's Q4_K / Q6_K encoders: the projections read back as the same blocks, and the
+    reference's decode of those blocks gives back the weights they were made from, to within the
+    format's resolution (16 levels per 32 values for Q4_K, 64 per 16 for Q6_K).  A byte or nibble
+    placed where the decoder does not look for it would leave the decoded rows uncorrelated with
+    the weights, so this pins the encoders' layout to the reference's decoder."""
+    from exactinfer_amd.gguf import GgufFile
+    m = TinyQwen3(seed=62, n_layer=1, n_embd=512, n_head=4, n_head_kv=2)
+    p = _write(tmp_path, m, tensors=qwen3_tensors(m, False, attn_type=attn_type))
+    rb = {12: 144, 14: 210}[tid]
+    with GgufFile(p) as g:
+        for name, rows in (("blk.0.attn_q.weight", 4 * 128), ("blk.0.attn_v.weight", 2 * 128)):
+            assert g.tensor_info(name)[0] == tid and g.tensor(name).shape == (rows, 512 // 256 * rb)
+        blocks = g.tensor("blk.0.attn_q.weight")
+    w = m.layers[0]["wqkv"][:4 * 128]
+    dq = orc.dequant(tid, blocks, 512).reshape(w.shape)
+    assert np.abs(dq - w).max() <= rel_bound * np.abs(w).max()
+    assert np.corrcoef(dq.ravel(), w.ravel())[0, 1] >= 0.995
+    model = TinyQwen3.from_gguf(p, dequant=orc.dequant)
+    assert np.array_equal(model.layers[0]["wqkv"][:4 * 128], dq)
