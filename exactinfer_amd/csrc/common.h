@@ -149,6 +149,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // With rope_dim = 128 (Qwen3) the partners i and i+64 sit in the same lane and the rotation
 // is done in registers; other rope_dims exchange partners through `dst`, 128 floats of
 // LDS scratch owned by this wave.  Returns the outputs for elements lane and lane+64.
+__device__ __forceinline__ void scale_rope_vals(float x0, float x1, float inv, float g0, float g1,
+                                                const float2* __restrict__ cs_row, int rope_dim, float* dst,
+                                                int lane, float* o0, float* o1);
+
 __device__ __forceinline__ void norm_rope_vals(float x0, float x1, float g0, float g1,
                                                const float2* __restrict__ cs_row, int rope_dim, float eps,
                                                float* dst, int lane, float* o0, float* o1) {
@@ -156,6 +160,73 @@ __device__ __forceinline__ void norm_rope_vals(float x0, float x1, float g0, flo
     double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
     ss = wave_sum_f64(ss);
     const float inv = (float)(1.0 / sqrt(ss / (double)kHeadDim + (double)eps));
+    scale_rope_vals(x0, x1, inv, g0, g1, cs_row, rope_dim, dst, lane, o0, o1);
+}
+
+// The norm factors of N heads at once (N a power of two, <= 64; lane l holds elements l and
+// l+64 of head j in x0[j], x1[j]).  The N sums of squares share one transposing butterfly: in
+// the steps over lane bits 5, 4, ... a lane keeps half of its remaining sums and adds its
+// partner's copy of that half (N/2 + N/4 + ... exchanges instead of 6N), then the single
+// remaining sum finishes the plain butterfly; lane L ends with the total of head
+// 32*b5 + 16*b4 + ... of its high bits (for N = 4: head 2*b5 + b4).  Every lane computes
+// 1/sqrt for its own head, so the double square root and division run once for all N heads,
+// and head j's factor is read from a lane that holds it.  The sum is a different tree order of
+// the same exact squares as norm_rope_vals; both match the sequential double sum to ~1e-16
+// relative.
+template <int N>
+__device__ __forceinline__ void head_inv(const float* x0, const float* x1, float eps, float* inv, int lane) {
+#pragma clang fp contract(off)
+    static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "a power of two");
+    double v[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = (double)x0[j] * (double)x0[j] + (double)x1[j] * (double)x1[j];
+    int n = N;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const bool up = (lane & m) != 0;
+        if (n > 1) {
+#pragma unroll
+            for (int i = 0; i < n / 2; ++i) {
+                const double send = up ? v[i] : v[i + n / 2];
+                const double keep = up ? v[i + n / 2] : v[i];
+                double r;
+                if (m == 32) r = lane_xor_f64<32>(send);
+                else if (m == 16) r = lane_xor_f64<16>(send);
+                else if (m == 8) r = lane_xor_f64<8>(send);
+                else if (m == 4) r = lane_xor_f64<4>(send);
+                else if (m == 2) r = lane_xor_f64<2>(send);
+                else r = lane_xor_f64<1>(send);
+                v[i] = keep + r;
+            }
+            n /= 2;
+        } else {
+            double r;
+            if (m == 32) r = lane_xor_f64<32>(v[0]);
+            else if (m == 16) r = lane_xor_f64<16>(v[0]);
+            else if (m == 8) r = lane_xor_f64<8>(v[0]);
+            else if (m == 4) r = lane_xor_f64<4>(v[0]);
+            else if (m == 2) r = lane_xor_f64<2>(v[0]);
+            else r = lane_xor_f64<1>(v[0]);
+            v[0] += r;
+        }
+    }
+    const float mine = (float)(1.0 / sqrt(v[0] / (double)kHeadDim + (double)eps));
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        // the lane whose high bits spell j: bit 5 - k of the lane is bit (log2 N - 1 - k) of j
+        int src = 0;
+#pragma unroll
+        for (int k = 0, b = N / 2; b >= 1; ++k, b >>= 1)
+            if (j & b) src |= 32 >> k;
+        inv[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), src));
+    }
+}
+
+// y = (x * inv) * gamma, then the NEOX rotation (see norm_rope_vals).
+__device__ __forceinline__ void scale_rope_vals(float x0, float x1, float inv, float g0, float g1,
+                                                const float2* __restrict__ cs_row, int rope_dim, float* dst,
+                                                int lane, float* o0, float* o1) {
+#pragma clang fp contract(off)
     const float y0 = (x0 * inv) * g0;
     const float y1 = (x1 * inv) * g1;
     if (rope_dim == kHeadDim) {

@@ -407,9 +407,21 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
             for (int i = Gr * D + lane; i < G * D; i += 64) qs[i] = 0.f;
         if constexpr (FUSED) {
             const float2* cs_row = reinterpret_cast<const float2*>(stage + 2 * D);
-            for (int g = 0; g < Gr; ++g) {  // in place: raw q -> normed, roped q
+            // in place: raw q -> normed, roped q; the G heads' norm factors together (padding
+            // heads are zeros: a finite factor, never used)
+            float x0[G], x1[G], inv[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                x0[g] = qs[g * D + lane];
+                x1[g] = qs[g * D + lane + 64];
+            }
+            head_inv<G>(x0, x1, a.eps, inv, lane);
+            const float qg0 = stage[lane], qg1 = stage[lane + 64];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                if (g >= Gr) break;
                 float o0, o1;
-                norm_rope_head(qs + g * D, stage, cs_row, a.rope_dim, a.eps, knew[2], lane, &o0, &o1);
+                scale_rope_vals(x0[g], x1[g], inv[g], qg0, qg1, cs_row, a.rope_dim, knew[2], lane, &o0, &o1);
                 qs[g * D + lane] = o0;
                 qs[g * D + lane + 64] = o1;
             }

@@ -76,14 +76,16 @@ __global__ __launch_bounds__(256) void k_qkv_prepare(float* __restrict__ qkv, lo
     const float qg0 = q_gamma[lane], qg1 = q_gamma[lane + 64];
     const float kg0 = k_gamma[lane], kg1 = k_gamma[lane + 64];
     const size_t kd = (size_t)HKV * kHeadDim;
+    float inv[kPrepHeads];  // the wave's heads normalised together (one double 1/sqrt)
+    head_inv<kPrepHeads>(x0, x1, eps, inv, lane);
 #pragma unroll
     for (int j = 0; j < kPrepHeads; ++j) {
         const int hh = h0 + j;
         if (hh >= NH) break;
         const bool is_k = hh >= H;
         float o0, o1;
-        norm_rope_vals(x0[j], x1[j], is_k ? kg0 : qg0, is_k ? kg1 : qg1, cs_row, rope_dim, eps, scratch[w], lane,
-                       &o0, &o1);
+        scale_rope_vals(x0[j], x1[j], inv[j], is_k ? kg0 : qg0, is_k ? kg1 : qg1, cs_row, rope_dim, scratch[w], lane,
+                        &o0, &o1);
         float* v = row + (size_t)hh * kHeadDim;
         v[lane] = o0;
         v[lane + 64] = o1;
