@@ -668,12 +668,15 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     merge_splits<G, kThreads>(a, head_slot, S, Gr, a.out + (size_t)seq * a.H * D + (size_t)h0 * D, tid, ring);
 }
 
-// Split combine as a separate launch: grid (n_seq * H), 128 threads (thread = d).  All
-// (m, l) and accumulator loads of the S splits are issued before any is used.  m is in
-// log2 units (the decode kernel's exp2 domain).
+// Split combine as a separate launch: grid (n_seq * H), 128 threads (thread = d).  Wave 0
+// issues the (m, l) loads of all S splits first, then every thread the accumulator loads of
+// its first 32 splits, so the weights are computed while the partials are still in flight
+// (loads return in issue order).  The weighted partials are summed in four interleaved
+// chains (split s into chain s % 4), added in a fixed order at the end.  m is in log2 units
+// (the decode kernel's exp2 domain).
 template <int G>
 __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
-    constexpr int D = kHeadDim;
+    constexpr int D = kHeadDim, B = 32, NA = 4, KM = kDecodeMaxSplits / 64;
     __shared__ float wsh[kDecodeMaxSplits];
     __shared__ float Lsh;
     const int hq = blockIdx.x % a.H, seq = blockIdx.x / a.H;
@@ -683,30 +686,33 @@ __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
     const size_t head_slot = (size_t)seq * a.HKV + kvh;
     const float* pml = reinterpret_cast<const float*>(a.rec + head_slot * S * kRec) + 2 + 2 * g;
     const float* pa = a.part_acc + (head_slot * S * G + g) * D + tid;
-    constexpr int B = 32;
-    float acc = 0.f;
+    float mv[KM], lv[KM];
+    if (tid < 64) {
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+            const int s = tid + 64 * k;
+            const float2 ml = s < S ? *reinterpret_cast<const float2*>(pml + (size_t)s * kRec)
+                                    : make_float2(-INFINITY, 0.f);
+            mv[k] = ml.x;
+            lv[k] = ml.y;
+        }
+    }
+    float acc[NA];
+#pragma unroll
+    for (int k = 0; k < NA; ++k) acc[k] = 0.f;
     for (int s0 = 0; s0 < S; s0 += B) {
         float v[B];
 #pragma unroll
         for (int b = 0; b < B; ++b) v[b] = pa[(size_t)min(s0 + b, S - 1) * G * D];
         if (s0 == 0) {
-            // weights: wave 0 reduces (m, l) over the splits
-            if (tid < 64) {
-                float mv[kDecodeMaxSplits / 64], lv[kDecodeMaxSplits / 64];
+            if (tid < 64) {  // weights: wave 0 reduces (m, l) over the splits
                 float M = -INFINITY;
 #pragma unroll
-                for (int k = 0; k < kDecodeMaxSplits / 64; ++k) {
-                    const int s = tid + 64 * k;
-                    const float2 ml = s < S ? *reinterpret_cast<const float2*>(pml + (size_t)s * kRec)
-                                            : make_float2(-INFINITY, 0.f);
-                    mv[k] = ml.x;
-                    lv[k] = ml.y;
-                    M = fmaxf(M, ml.x);
-                }
+                for (int k = 0; k < KM; ++k) M = fmaxf(M, mv[k]);
                 M = wave_max(M);
                 float L = 0.f;
 #pragma unroll
-                for (int k = 0; k < kDecodeMaxSplits / 64; ++k) {
+                for (int k = 0; k < KM; ++k) {
                     const int s = tid + 64 * k;
                     const float wv = mv[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv[k] - M);  // empty split: skipped
                     if (s < S) wsh[s] = wv;
@@ -719,9 +725,10 @@ __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
         }
 #pragma unroll
         for (int b = 0; b < B; ++b)
-            if (s0 + b < S) acc = fmaf(wsh[s0 + b], v[b], acc);
+            if (s0 + b < S) acc[b % NA] = fmaf(wsh[s0 + b], v[b], acc[b % NA]);
     }
-    a.out[(size_t)seq * a.H * D + (size_t)hq * D + tid] = Lsh > 0.f ? acc / Lsh : 0.f;  // kv_len 0: zeros
+    const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    a.out[(size_t)seq * a.H * D + (size_t)hq * D + tid] = Lsh > 0.f ? sum / Lsh : 0.f;  // kv_len 0: zeros
 }
 
 __global__ void k_ws_clear(uint32_t* p, size_t n) {
