@@ -522,13 +522,18 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
             if (r == 0 && j == 0) mw[w][g] = mn;
         }
         __builtin_amdgcn_wave_barrier();
+        if (t0 == tw0) {  // the wave's first tile: nothing accumulated yet, nothing to rescale
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mn = mw[w][g];
-            const float corr = __builtin_amdgcn_exp2f(m[g] - mn);
-            m[g] = mn;
-            acc[g].x *= corr;
-            acc[g].y *= corr;
+            for (int g = 0; g < G; ++g) m[g] = mw[w][g];
+        } else {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float mn = mw[w][g];
+                const float corr = __builtin_amdgcn_exp2f(m[g] - mn);
+                m[g] = mn;
+                acc[g].x *= corr;
+                acc[g].y *= corr;
+            }
         }
         // ---- values: acc[g][d] += p[row][g] * V[row][d], once the V rows have landed
         if (next_flying) wait_vmcnt<kTile>();
@@ -614,24 +619,30 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
         return;
     }
 
-    // unnormalised partial of this split: acc rows, then the split's record line (written whole
-    // by one instruction, so the line is valid in the L2 without a fill)
+    // unnormalised partial of this split: acc rows, then the split's record line: for k_combine
+    // the (m, l) pairs straight from the threads that hold them; for the in-kernel merge the
+    // whole line by one instruction (valid in the L2 without a fill), with this XCD's id
     if (tid < NCOL && gcol < Gr) *reinterpret_cast<float4*>(a.part_acc + (slot * G + gcol) * D + 4 * d4) = o;
+    const bool merging = a.merge_in_kernel;
+    if (!merging) {  // k_combine merges in a second launch and reads only the (m, l) words of real heads
+        if (tid < NCOL && d4 == 0 && gcol < Gr)
+            *reinterpret_cast<float2*>(my_rec + 2 + 2 * gcol) = make_float2(Mw, Lw);
+        return;
+    }
     __shared__ float mlsh[2 * G];
     __shared__ int is_last;
     if (tid < NCOL && d4 == 0) {
         mlsh[2 * gcol] = Mw;
         mlsh[2 * gcol + 1] = Lw;
     }
-    const bool merging = a.merge_in_kernel;
-    if (merging) wait_vmcnt<0>();  // this thread's acc stores are in the L2 before the record is
+    wait_vmcnt<0>();  // this thread's acc stores are in the L2 before the record is
     __syncthreads();
     if (w == 0) {
         uint32_t xcc = 0;
-        if (merging) asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
         if (lane < kRec)
             my_rec[lane] = lane == 1 ? xcc : lane >= 2 && lane < 2 + 2 * G ? __float_as_uint(mlsh[lane - 2]) : 0u;
-        if (merging) {
+        {
             // In-kernel merge.  Every split of the unit ran on this XCD, so the partials meet in
             // its L2: a store is acknowledged by the L2 (vmcnt), and loads that miss the CU's L1
             // read it there.  Once its partial and record are acknowledged, a workgroup counts
@@ -662,7 +673,6 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
             if (lane == 0) is_last = last;
         }
     }
-    if (!merging) return;  // k_combine merges the splits in a second launch
     __syncthreads();
     if (!is_last) return;
     merge_splits<G, kThreads>(a, head_slot, S, Gr, a.out + (size_t)seq * a.H * D + (size_t)h0 * D, tid, ring);
