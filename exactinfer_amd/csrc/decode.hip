@@ -753,15 +753,19 @@ static int pow2_ceil(long x) {
 }
 
 DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged) {
-    // One workgroup per (sequence, KV head) streams the most bytes per launch and needs no
-    // combine; keys are split only as far as it takes to reach about one workgroup per CU
-    // (256): chunk = max_kv / ceil(256 / (n_seq * HKV)), rounded up to a power of two >= 128
-    // (128 fills every wave's two-tile ring once).  The split count stays within the
-    // combine's table.
+    // Keys are split as far as it takes to reach about one workgroup per CU (256): chunk =
+    // max_kv / ceil(256 / (n_seq * HKV)), rounded up to a power of two >= 128 (128 fills every
+    // wave's two-tile ring once), and at most 1024 keys: a batch of ragged sequences (the plan
+    // sees only max_kv; the lengths are on the device) then spreads its long sequences over
+    // many workgroups instead of leaving a few 8192-key units running alone at the end of the
+    // launch (configs[4]-shaped batches, lengths U[256, 8192]: +1% to +10% over four length
+    // draws, contiguous and paged alike).  Splits of a 1024-key chunk merge inside the launch,
+    // so the cap adds no launch.  The split count stays within the combine's table.
     const long units = (long)n_seq * HKV;
     const long want = units >= 256 ? 1 : (256 + units - 1) / units;
     int chunk = pow2_ceil(((long)max_kv + want - 1) / want);
     if (chunk < 128) chunk = 128;
+    if (chunk > kDecodeMaxChunk) chunk = kDecodeMaxChunk;
     if (const char* env = std::getenv("EI_DECODE_CHUNK")) {  // tuning override (multiple of 64)
         const int v = std::atoi(env);
         if (v >= 64 && v % 64 == 0) chunk = v;

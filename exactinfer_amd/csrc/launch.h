@@ -60,6 +60,7 @@ struct DecodePlan {
 };
 constexpr int kDecodeMaxSplits = 256;
 constexpr int kDecodePagedMaxChunk = 8192;  // 4 waves x 128 tiles of 16 keys
+constexpr int kDecodeMaxChunk = 1024;       // longer keys are split (ragged batches balance across CUs)
 DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged);
 size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv);
 // the call's partials: accumulators at 0, then the split records (ending at `partials`)

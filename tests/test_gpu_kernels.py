@@ -489,9 +489,9 @@ def test_decode_paged_matches_reference(orc, gpu, bs):
 
 @pytest.mark.parametrize("bs", [16, 64])
 def test_decode_paged_long_sequences_whole_chunks(orc, gpu, bs):
-    """32 sequences x 8 KV heads = 256 units: the plan runs each (sequence, KV head) as one
-    8192-key chunk, so a wave walks up to 128 tiles and reads the cache rows of tiles 64..127
-    from its second row register."""
+    """32 sequences x 8 KV heads = 256 units with a workspace planned for 1024 keys: one split
+    per unit, which takes every key past the plan (lengths up to 8192), so a wave walks up to
+    128 tiles and reads the cache rows of tiles 64..127 from its second row register."""
     H, HKV = 8, 8
     rng = np.random.default_rng(70 + bs)
     lens = np.concatenate([np.array([8192, 6000, 4097, 5000], np.int32), rng.integers(1, 200, 28).astype(np.int32)])
@@ -499,7 +499,7 @@ def test_decode_paged_long_sequences_whole_chunks(orc, gpu, bs):
     pool_k, pool_v = _cache(orc, nblocks * bs, HKV, 5000 + bs)
     q = orc.normal((len(lens), H * D), 5001)
     shape = gpu.AttnShape(H, HKV)
-    ws = gpu.DecodeWorkspace(len(lens), H, HKV, max_kv=8192)
+    ws = gpu.DecodeWorkspace(len(lens), H, HKV, max_kv=1024)
     out = _host(gpu.attn_decode_paged(_dev(q), _dev(pool_k), _dev(pool_v), _dev(table), bs, _dev(lens), shape, ws))
     for s_, n in enumerate(lens):
         kk, vv = _gather(pool_k, table, s_, n, bs), _gather(pool_v, table, s_, n, bs)
