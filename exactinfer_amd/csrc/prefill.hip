@@ -31,8 +31,9 @@
 // with this tile's P.V chains, and the next tiles' DMA instructions are issued between them
 // (VMEM work outside the stream idles the pipe).  When one unit pair per KV head would not
 // fill the CUs (short chunks at long positions, GQA groups under 4 heads;
-// ei_attn_prefill_split) the key range of every unit is further split over ksplit
-// workgroups whose unnormalised shares k_prefill_combine merges.
+// ei_attn_prefill_split) the pair's key tiles are split over ksplit workgroups of equal cost
+// (a share that crosses from one unit to the other pays a second pass), whose unnormalised
+// shares k_prefill_combine merges.
 //
 // K/V tiles (32 keys) reach LDS by LDS DMA (global_load_lds_dwordx4) straight from the
 // cache, two tiles ahead for K and one for V, per key group:
@@ -78,6 +79,7 @@ constexpr int kKS = 2;                           // key groups per workgroup
 constexpr float kLazy = 8.f;                     // lazy-rescale threshold (log2 units)
 constexpr int kXchF = 34;                        // floats per lane exchanged by the merge
 constexpr int kSlots = 4;                        // query slots (waves) per key group
+constexpr int kPassTiles = 3;                    // a pass's fixed cost, in tiles (key-share balance; 1..4 tried)
 
 // n / d for small d (1..8) and n * d < 2^32 as one multiply-high: the per-pass index math
 // runs on the scalar unit, which the eight waves of a CU share, so a division loop per use
@@ -277,10 +279,38 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         }
     };
     const int u_second = nu - 1 - pair;  // the pass-1 unit (none when it equals pair)
+    // Key shares.  The pair's tiles, unit `pair`'s then unit `u_second`'s, are cut into ksplit
+    // contiguous shares of equal cost, where the boundary between the units counts as
+    // kPassTiles extra tiles: a share that crosses it runs two passes (q staging, first tiles,
+    // key-group merge and store twice), so it gets that many fewer tiles, and every other
+    // share runs one pass.  A share with no tile of a unit skips that unit's pass and marks its
+    // rows empty for k_prefill_combine.  With ksplit = 1 the one share is both whole units.
+    auto unit_tiles = [&](int uu) {
+        const int ql = fdiv(min(kSlots * uu + kSlots - 1, nslot - 1), fG);
+        return (pos0 + min(B, ql * kQB + kQB) + kKT - 1) / kKT;
+    };
+    const int n0 = unit_tiles(pair), n1 = u_second != pair ? unit_tiles(u_second) : 0;
+    const int pen = n1 > 0 ? kPassTiles : 0;
+    const int n_all = n0 + n1 + pen;
+    auto real_tile = [&](int x) { return x <= n0 ? x : (x <= n0 + pen ? n0 : x - pen); };
+    // (wave-uniform: readfirstlane keeps them in scalar registers, the vector budget is full)
+    const int share_lo = __builtin_amdgcn_readfirstlane(real_tile(fdiv(split * n_all, fK)));
+    const int share_hi = __builtin_amdgcn_readfirstlane(real_tile(fdiv((split + 1) * n_all, fK)));
+    const int r0 = max(min(share_hi, n0) - share_lo, 0), r1 = max(share_hi - max(share_lo, n0), 0);
+    // a unit of the pair without tiles in this share: its rows are marked empty, its pass skipped
+    for (int e = 0; e < 2; ++e) {
+        const int ue = e == 0 ? pair : u_second;
+        if ((e == 0 ? r0 : r1) > 0 || (e == 1 && ue == pair)) continue;
+        const int sle = kSlots * ue + hw, qbe = fdiv(sle, fG), be = qbe * kQB + col;
+        if (sle < nslot && be < B && hh == 0 && grp == 0)
+            *reinterpret_cast<float2*>(part_ml + ((size_t)split * B * H + (size_t)be * H + kvh * G + sle - qbe * G) * 2) =
+                make_float2(-INFINITY, 0.f);
+    }
+    const int npass = (r0 > 0) + (r1 > 0);
 
-    for (int pass = 0; pass < 2; ++pass) {
-        const int u = pass == 0 ? pair : u_second;
-        if (pass == 1 && u == pair) break;
+    for (int pass = 0; pass < npass; ++pass) {
+        const bool first_unit = pass == 0 && r0 > 0;  // this pass runs unit `pair`
+        const int u = first_unit ? pair : u_second;
         const int sl = kSlots * u + hw;            // this wave's slot (wave-uniform)
         const bool live = sl < nslot;
         const int qb = fdiv(sl, fG), h = kvh * G + sl - qb * G;
@@ -298,8 +328,9 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         const int T = pos0 + min(B, qb_last * kQB + kQB);  // keys seen by the unit's last query
         const int ntile = (T + kKT - 1) / kKT;
         const int nfull = live ? (pos0 + qb * kQB + 1) / kKT : ntile;  // tiles below this wave's diagonal
-        const int kt_lo = fdiv(split * ntile, fK);       // this workgroup's tiles: [kt_lo, kt_hi)
-        const int nrange = fdiv((split + 1) * ntile, fK) - kt_lo;
+        // this workgroup's tiles of the unit: [kt_lo, kt_lo + nrange)
+        const int kt_lo = __builtin_amdgcn_readfirstlane(first_unit ? share_lo : max(share_lo, n0) - n0);
+        const int nrange = __builtin_amdgcn_readfirstlane(first_unit ? r0 : r1);
         const int n_it = (nrange + kKS - 1) / kKS;
         const int n_mine = (nrange - grp + kKS - 1) / kKS;  // tiles of this key group
 
