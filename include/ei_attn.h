@@ -216,9 +216,9 @@ int ei_attn_prefill_split(ei_stream_t stream, const float* q, long q_stride, flo
  * src/cuda/model_cuda.cu:1800-1820 in two launches (plus the key-split merge when planned).
  * qkv rows [Q|K|V] are raw projections: the K heads are normed + roped in place and appended
  * with the V rows to cache rows *pos_dev + b (as ei_qkv_prepare does).  With rope_dim = 128
- * (every Qwen3) and a plan of at most two key shares, the Q heads are left raw in qkv and
+ * (every Qwen3) and a plan of at most four key shares, the Q heads are left raw in qkv and
  * normed + roped inside the attention kernel where it stages them; otherwise (a partial
- * rope_dim, or short chunks at long positions split into more shares) they are normed in
+ * rope_dim, or a plan of more shares) they are normed in
  * place by the prologue first.  Same workspace and plan as ei_attn_prefill_split;
  * out [B][n_head][128]. */
 int ei_prefill_step(ei_stream_t stream, float* qkv, long row_stride, float* out, float* kc, float* vc,
