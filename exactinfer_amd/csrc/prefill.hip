@@ -91,6 +91,32 @@ __device__ __forceinline__ FastDiv fast_div(uint32_t d) { return {d == 1 ? 0u : 
 __device__ __forceinline__ int fdiv(int n, FastDiv f) {
     return f.d == 1 ? n : (int)__umulhi((uint32_t)n, f.m);
 }
+// Key shares.  A workgroup runs units `pair` and nu-1-pair (causal balance).  With ksplit
+// shares, the pair's tiles, unit pair's then unit nu-1-pair's, are cut into ksplit contiguous
+// shares of equal cost, where the boundary between the units counts as kPassTiles extra tiles:
+// a share that crosses it runs two passes (q staging, first tiles, key-group merge and store
+// twice), so it gets that many fewer tiles, and every other share runs one pass.  Share
+// `split` holds tiles [lo0, lo0 + r0) of unit pair and [lo1, lo1 + r1) of unit nu-1-pair; a
+// unit without tiles in a share has no pass there and no partial, and k_prefill_combine,
+// which evaluates the same cut, does not read one.  With ksplit = 1 the share is both units.
+__device__ __forceinline__ int prefill_unit_tiles(int u, int pos0, int B, int nslot, FastDiv fG) {
+    const int ql = fdiv(min(kSlots * u + kSlots - 1, nslot - 1), fG);  // the unit's last block
+    return (pos0 + min(B, ql * kQB + kQB) + kKT - 1) / kKT;
+}
+__device__ __forceinline__ void prefill_share(int pair, int u_second, int split, FastDiv fK, int pos0, int B,
+                                              int nslot, FastDiv fG, int& lo0, int& r0, int& lo1, int& r1) {
+    const int n0 = prefill_unit_tiles(pair, pos0, B, nslot, fG);
+    const int n1 = u_second != pair ? prefill_unit_tiles(u_second, pos0, B, nslot, fG) : 0;
+    const int pen = n1 > 0 ? kPassTiles : 0;
+    const int n_all = n0 + n1 + pen;
+    auto real_tile = [&](int x) { return x <= n0 ? x : (x <= n0 + pen ? n0 : x - pen); };
+    const int lo = real_tile(fdiv(split * n_all, fK)), hi = real_tile(fdiv((split + 1) * n_all, fK));
+    lo0 = lo;
+    r0 = max(min(hi, n0) - lo, 0);
+    lo1 = max(lo, n0) - n0;
+    r1 = max(hi - max(lo, n0), 0);
+}
+
 // LDS (plain kernel): the four K tile buffers (two per key group) from 0; the merge exchange
 // area from 0 as well (used only after the unit's last tile); the four V tile buffers and,
 // overlapping them, the q staging area (the unit's 4 x 32 query rows, padded like K rows)
@@ -279,33 +305,14 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         }
     };
     const int u_second = nu - 1 - pair;  // the pass-1 unit (none when it equals pair)
-    // Key shares.  The pair's tiles, unit `pair`'s then unit `u_second`'s, are cut into ksplit
-    // contiguous shares of equal cost, where the boundary between the units counts as
-    // kPassTiles extra tiles: a share that crosses it runs two passes (q staging, first tiles,
-    // key-group merge and store twice), so it gets that many fewer tiles, and every other
-    // share runs one pass.  A share with no tile of a unit skips that unit's pass and marks its
-    // rows empty for k_prefill_combine.  With ksplit = 1 the one share is both whole units.
-    auto unit_tiles = [&](int uu) {
-        const int ql = fdiv(min(kSlots * uu + kSlots - 1, nslot - 1), fG);
-        return (pos0 + min(B, ql * kQB + kQB) + kKT - 1) / kKT;
-    };
-    const int n0 = unit_tiles(pair), n1 = u_second != pair ? unit_tiles(u_second) : 0;
-    const int pen = n1 > 0 ? kPassTiles : 0;
-    const int n_all = n0 + n1 + pen;
-    auto real_tile = [&](int x) { return x <= n0 ? x : (x <= n0 + pen ? n0 : x - pen); };
-    // (wave-uniform: readfirstlane keeps them in scalar registers, the vector budget is full)
-    const int share_lo = __builtin_amdgcn_readfirstlane(real_tile(fdiv(split * n_all, fK)));
-    const int share_hi = __builtin_amdgcn_readfirstlane(real_tile(fdiv((split + 1) * n_all, fK)));
-    const int r0 = max(min(share_hi, n0) - share_lo, 0), r1 = max(share_hi - max(share_lo, n0), 0);
-    // a unit of the pair without tiles in this share: its rows are marked empty, its pass skipped
-    for (int e = 0; e < 2; ++e) {
-        const int ue = e == 0 ? pair : u_second;
-        if ((e == 0 ? r0 : r1) > 0 || (e == 1 && ue == pair)) continue;
-        const int sle = kSlots * ue + hw, qbe = fdiv(sle, fG), be = qbe * kQB + col;
-        if (sle < nslot && be < B && hh == 0 && grp == 0)
-            *reinterpret_cast<float2*>(part_ml + ((size_t)split * B * H + (size_t)be * H + kvh * G + sle - qbe * G) * 2) =
-                make_float2(-INFINITY, 0.f);
-    }
+    // this workgroup's share of the pair (prefill_share); wave-uniform: readfirstlane keeps the
+    // values in scalar registers, the vector budget is full
+    int lo0, r0, lo1, r1;
+    prefill_share(pair, u_second, split, fK, pos0, B, nslot, fG, lo0, r0, lo1, r1);
+    lo0 = __builtin_amdgcn_readfirstlane(lo0);
+    r0 = __builtin_amdgcn_readfirstlane(r0);
+    lo1 = __builtin_amdgcn_readfirstlane(lo1);
+    r1 = __builtin_amdgcn_readfirstlane(r1);
     const int npass = (r0 > 0) + (r1 > 0);
 
     for (int pass = 0; pass < npass; ++pass) {
@@ -328,9 +335,8 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         const int T = pos0 + min(B, qb_last * kQB + kQB);  // keys seen by the unit's last query
         const int ntile = (T + kKT - 1) / kKT;
         const int nfull = live ? (pos0 + qb * kQB + 1) / kKT : ntile;  // tiles below this wave's diagonal
-        // this workgroup's tiles of the unit: [kt_lo, kt_lo + nrange)
-        const int kt_lo = __builtin_amdgcn_readfirstlane(first_unit ? share_lo : max(share_lo, n0) - n0);
-        const int nrange = __builtin_amdgcn_readfirstlane(first_unit ? r0 : r1);
+        const int kt_lo = first_unit ? lo0 : lo1;  // this workgroup's tiles of the unit: [kt_lo, kt_lo + nrange)
+        const int nrange = first_unit ? r0 : r1;
         const int n_it = (nrange + kKS - 1) / kKS;
         const int n_mine = (nrange - grp + kKS - 1) / kKS;  // tiles of this key group
 
@@ -615,15 +621,27 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
 // shares (m = -inf) skipped.
 __global__ __launch_bounds__(128) void k_prefill_combine(const float* __restrict__ part_o,
                                                          const float* __restrict__ part_ml, float* __restrict__ out,
-                                                         int rows, int ksplit) {
+                                                         int rows, int ksplit, const int* __restrict__ pos_dev, int B,
+                                                         int H, int HKV) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 5), d4 = threadIdx.x & 31;
     if (row >= rows) return;
-    // every share's (m, l) and accumulator piece is loaded before any is used: one round trip
+    // the row's unit and pair, as k_prefill numbers them; the shares holding tiles of that unit
+    const int G = H / HKV, b = row / H, hq = row - b * H, g = hq % G;
+    const int nb = (B + kQB - 1) / kQB, nslot = G * nb, nu = (nslot + kSlots - 1) / kSlots;
+    const int u = ((b / kQB) * G + g) / kSlots, pair = min(u, nu - 1 - u);
+    const FastDiv fG = fast_div((uint32_t)G), fK = fast_div((uint32_t)ksplit);
+    const int pos0 = *pos_dev;
+    // the covered shares' (m, l) and accumulator pieces are loaded before any is used: one
+    // round trip, and no read of a share without tiles of this unit
     float2 ml[kPrefillMaxSplit];
     float4 v[kPrefillMaxSplit];
 #pragma unroll
     for (int s = 0; s < kPrefillMaxSplit; ++s) {
-        if (s >= ksplit) break;
+        ml[s] = make_float2(-INFINITY, 0.f);
+        if (s >= ksplit) continue;
+        int lo0, r0, lo1, r1;
+        prefill_share(pair, nu - 1 - pair, s, fK, pos0, B, nslot, fG, lo0, r0, lo1, r1);
+        if ((u == pair ? r0 : r1) == 0) continue;
         const size_t slot = (size_t)s * rows + row;
         ml[s] = *reinterpret_cast<const float2*>(part_ml + slot * 2);
         v[s] = *reinterpret_cast<const float4*>(part_o + slot * kHeadDim + 4 * d4);
@@ -738,7 +756,7 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
     if (e != hipSuccess) return e;
     if (ksplit > 1) {
         const int rows = B * H;
-        k_prefill_combine<<<(rows + 3) / 4, 128, 0, st>>>(part_o, part_ml, out, rows, ksplit);
+        k_prefill_combine<<<(rows + 3) / 4, 128, 0, st>>>(part_o, part_ml, out, rows, ksplit, pos_dev, B, H, HKV);
     }
     return hipGetLastError();
 }
