@@ -100,6 +100,20 @@ float* HipAttention::vcache(int l) const {
     return kv_ + (size_t(c_.n_layer) + size_t(l)) * size_t(n_ctx_) * kd;
 }
 
+void HipAttention::project(const float* x, long x_stride, int n_embd, const float* attn_norm, const void* w,
+                           int w_type, int n_out, float* qkv, long qkv_stride) {
+    if (B_ <= 0) throw std::logic_error("project() before begin_chunk()");
+    if (n_embd <= 0) throw std::invalid_argument("n_embd");
+    int per = 24576 / n_embd;  // rows per launch (ei_qkv_project stages them in LDS)
+    if (per > 4) per = 4;
+    if (per < 1) throw std::invalid_argument("n_embd too large for the projection");
+    for (int b = 0; b < B_; b += per) {
+        const int rows = B_ - b < per ? B_ - b : per;
+        check(ei_qkv_project(stream_, x + size_t(b) * x_stride, x_stride, rows, n_embd, attn_norm, c_.eps, w, w_type,
+                             n_out, qkv + size_t(b) * qkv_stride, qkv_stride));
+    }
+}
+
 void HipAttention::layer(int l, float* qkv, long qkv_stride, const float* q_norm, const float* k_norm, float* att) {
     if (l < 0 || l >= c_.n_layer) throw std::out_of_range("layer index");
     if (B_ <= 0) throw std::logic_error("layer() before begin_chunk()");

@@ -59,6 +59,18 @@ public:
     // the GPU).
     void layer(int l, float* qkv, long qkv_stride, const float* q_norm, const float* k_norm, float* att);
 
+    // Attention RMSNorm + QKV projection of the current chunk's B rows, the step before layer()
+    // (k_rmsnorm + linear(h, L.qkv, ...), src/cuda/model_cuda.cu:1797-1799; the CPU path's
+    // rmsnorm + matvec, src/model.cpp:176-179):
+    //   x [B][n_embd] residual rows (row stride x_stride), attn_norm [n_embd] (device);
+    //   w: n_out rows of n_embd weights in the GGUF row layout of w_type (EI_W_F32, EI_W_F16,
+    //   EI_W_Q8_0, EI_W_Q4_K, EI_W_Q6_K); the fused [Wq | Wk | Wv] with n_out = (H + 2 HKV) * 128,
+    //   or one segment of it (qkv then points at the segment's first column);
+    //   qkv [B][...] output rows (row stride qkv_stride), left raw for layer().
+    // Runs ei_qkv_project over groups of rows (at most min(4, 24576 / n_embd) per launch).
+    void project(const float* x, long x_stride, int n_embd, const float* attn_norm, const void* w, int w_type,
+                 int n_out, float* qkv, long qkv_stride);
+
     // Device views of layer l's cache, [n_ctx][n_head_kv][128] fp32.
     float* kcache(int l) const;
     float* vcache(int l) const;

@@ -10,6 +10,9 @@ extern "C" {
 void orc_fill_normal(float* out, size_t n, uint64_t seed, uint64_t offset);
 void orc_fill_gamma(float* out, size_t n, uint64_t seed);
 void orc_rmsnorm(float* out, const float* x, const float* w, int n, float eps);
+/* y[r] = dot(row r of w, x) for `rows` rows of n values in the GGUF layout of `type` (0 F32, 1 F16, 8 Q8_0,
+ * 12 Q4_K, 14 Q6_K) */
+void orc_matvec(int type, const void* w, const float* x, float* y, long rows, long n);
 void orc_rope_inv_freq(double* out, int rope_dim, double base);
 void orc_rope(float* v, int pos, int dim, const double* inv_freq);
 void orc_rope_table(float* cs, int n_ctx, int rope_dim, double base);

@@ -10,10 +10,14 @@
 // it is within 1e-5 of float64 attention and no farther from it than the reference is
 // (the rule of tests/parity.py).
 //
-// Usage: engine_test <n_layer> <n_head> <n_head_kv> <prompt> <max_batch> <decode_steps> <n_ctx> [graph]
+// Usage: engine_test <n_layer> <n_head> <n_head_kv> <prompt> <max_batch> <decode_steps> <n_ctx> [graph] [project]
 // With "graph", decode steps after the first replay one captured hipGraph of all layers' attention
 // sub-steps, the way the reference replays its decode step (src/cuda/model_cuda.cu:1848-1859): the
 // device position advances between replays, the graph itself never changes.
+// With "project", the raw QKV rows are not drawn at random: every token's rows of every layer come
+// from HipAttention::project (attention RMSNorm + QKV projection on the GPU) of seeded residual
+// rows and F32 weights, in the same chunks, checked against the CPU path's rmsnorm + matvec
+// (src/model.cpp:176-179) within 1e-5 of the row's rms; the attention checks then run on them.
 // Prints one JSON line; exit status 0 when every check passes.
 #include <hip/hip_runtime.h>
 
@@ -26,6 +30,7 @@
 #include <vector>
 
 #include "../../exactinfer_amd/host/hip_attention.h"
+#include "../../include/ei_attn.h"
 #include "../../oracle/oracle.h"
 
 static void hc(hipError_t e) {
@@ -48,11 +53,16 @@ static double rel_err_row(const float* got, const float* ref, int n) {
 }
 
 int main(int argc, char** argv) {
-    if (argc != 8 && !(argc == 9 && std::string(argv[8]) == "graph")) {
-        std::fprintf(stderr, "usage: engine_test n_layer n_head n_head_kv prompt max_batch decode_steps n_ctx [graph]\n");
+    bool use_graph = false, use_project = false, bad_args = argc < 8;
+    for (int i = 8; i < argc; ++i) {
+        if (std::string(argv[i]) == "graph") use_graph = true;
+        else if (std::string(argv[i]) == "project") use_project = true;
+        else bad_args = true;
+    }
+    if (bad_args) {
+        std::fprintf(stderr, "usage: engine_test n_layer n_head n_head_kv prompt max_batch decode_steps n_ctx [graph] [project]\n");
         return 2;
     }
-    const bool use_graph = argc == 9;
     ei::AttnConfig cfg;
     cfg.n_layer = std::atoi(argv[1]);
     cfg.n_head = std::atoi(argv[2]);
@@ -73,6 +83,53 @@ int main(int argc, char** argv) {
     std::vector<float> raw(size_t(L) * total * QKV);
     orc_fill_normal(raw.data(), raw.size(), 7, 0);
     auto raw_row = [&](int l, int t) { return raw.data() + (size_t(l) * total + t) * QKV; };
+
+    // ---- optional: the raw rows from HipAttention::project, in the engine's chunks
+    double worst_proj = 0;
+    if (use_project) {
+        const int E = 1024;
+        std::vector<float> x(size_t(L) * total * E), w(size_t(L) * QKV * E), g(size_t(L) * E);
+        orc_fill_normal(x.data(), x.size(), 11, 0);
+        orc_fill_normal(w.data(), w.size(), 12, 0);
+        for (float& v : w) v *= 0.05f;
+        for (int l = 0; l < L; ++l) orc_fill_gamma(g.data() + size_t(l) * E, E, 13 + l);
+        hipStream_t ps;
+        hc(hipStreamCreate(&ps));
+        {
+            ei::HipAttention eng(cfg, n_ctx, max_batch, ps);
+            float *d_x, *d_w, *d_g, *d_q;
+            hc(hipMalloc(&d_x, size_t(max_batch) * E * 4));
+            hc(hipMalloc(&d_w, w.size() * 4));
+            hc(hipMalloc(&d_g, g.size() * 4));
+            hc(hipMalloc(&d_q, size_t(max_batch) * QKV * 4));
+            hc(hipMemcpy(d_w, w.data(), w.size() * 4, hipMemcpyHostToDevice));
+            hc(hipMemcpy(d_g, g.data(), g.size() * 4, hipMemcpyHostToDevice));
+            std::vector<float> h(E), ref(QKV);
+            auto project_chunk = [&](int pos0, int B) {
+                eng.begin_chunk(pos0, B);
+                for (int l = 0; l < L; ++l) {
+                    hc(hipMemcpyAsync(d_x, x.data() + (size_t(l) * total + pos0) * E, size_t(B) * E * 4,
+                                      hipMemcpyHostToDevice, ps));
+                    eng.project(d_x, E, E, d_g + size_t(l) * E, d_w + size_t(l) * QKV * E, EI_W_F32, QKV, d_q, QKV);
+                    hc(hipMemcpyAsync(raw_row(l, pos0), d_q, size_t(B) * QKV * 4, hipMemcpyDeviceToHost, ps));
+                    hc(hipStreamSynchronize(ps));
+                    for (int b = 0; b < B; ++b) {
+                        orc_rmsnorm(h.data(), x.data() + (size_t(l) * total + pos0 + b) * E, g.data() + size_t(l) * E,
+                                    E, cfg.eps);
+                        orc_matvec(0, w.data() + size_t(l) * QKV * E, h.data(), ref.data(), QKV, E);
+                        worst_proj = std::max(worst_proj, rel_err_row(raw_row(l, pos0 + b), ref.data(), QKV));
+                    }
+                }
+            };
+            for (int p = 0; p < prompt; p += max_batch) project_chunk(p, std::min(max_batch, prompt - p));
+            for (int t = prompt; t < total; ++t) project_chunk(t, 1);
+            hc(hipFree(d_x));
+            hc(hipFree(d_w));
+            hc(hipFree(d_g));
+            hc(hipFree(d_q));
+        }
+        hc(hipStreamDestroy(ps));
+    }
 
     // ---- CPU reference, one token at a time
     std::vector<float> rk(size_t(L) * n_ctx * KD, 0.f), rv(size_t(L) * n_ctx * KD, 0.f);
@@ -209,11 +266,12 @@ int main(int argc, char** argv) {
         hc(hipFree(d_kg));
     }
     hc(hipStreamDestroy(st));
-    const bool ok = worst <= 1e-5 && caches_exact && threw_ok;
+    const bool ok = worst <= 1e-5 && caches_exact && threw_ok && worst_proj <= 1e-5;
     std::printf("{\"ok\": %s, \"max_rel_err\": %.3e, \"f64_fallback_rows\": %d, \"caches_bit_exact\": %s, "
                 "\"out_of_range_thrown\": %s, \"layers\": %d, \"prompt\": %d, \"max_batch\": %d, "
-                "\"decode_steps\": %d, \"graph\": %s}\n",
+                "\"decode_steps\": %d, \"graph\": %s, \"project\": %s, \"project_max_rel_err\": %.3e}\n",
                 ok ? "true" : "false", worst, fallback_rows, caches_exact ? "true" : "false",
-                threw_ok ? "true" : "false", L, prompt, max_batch, steps, use_graph ? "true" : "false");
+                threw_ok ? "true" : "false", L, prompt, max_batch, steps, use_graph ? "true" : "false",
+                use_project ? "true" : "false", worst_proj);
     return ok ? 0 : 1;
 }

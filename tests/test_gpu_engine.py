@@ -53,3 +53,12 @@ def test_decode_steps_replay_one_captured_graph():
     rc, res = _run(2, 32, 8, 200, 128, 40, 300, "graph")
     assert rc == 0 and res["ok"] and res["graph"], res
     assert res["caches_bit_exact"]
+
+
+def test_projection_then_attention_per_chunk():
+    """The engine's QKV projection (HipAttention::project: attention RMSNorm + fused QKV GEMV on the
+    GPU, in row groups) on seeded residual rows, prompt chunks of 100 rows then decode steps; each
+    chunk's rows within 1e-5 of the CPU path's rmsnorm + matvec, then the attention checks on them."""
+    rc, res = _run(2, 32, 8, 260, 100, 6, 300, "project")
+    assert rc == 0 and res["ok"] and res["project"], res
+    assert res["project_max_rel_err"] <= 1e-5 and res["caches_bit_exact"]
