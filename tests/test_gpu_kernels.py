@@ -340,6 +340,30 @@ def test_prefill_split_matches_reference_attention(orc, gpu, H, HKV, B, pos0, ma
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("ksplit", [2, 3, 5, 8])
+@pytest.mark.parametrize("H,HKV,B,pos0", [(12, 4, 77, 1500), (8, 1, 300, 0), (40, 8, 33, 3000), (16, 8, 512, 700)])
+def test_prefill_forced_share_counts(orc, gpu, monkeypatch, ksplit, H, HKV, B, pos0):
+    """Every share count on shapes that stress the cost-cut shares (a pair's tiles cut into shares
+    of equal cost, the unit boundary counting extra): ragged last blocks, GQA groups of 3 and 8, a
+    single KV head, a middle unit without a partner, chunks at position 0 (short units, shares
+    without tiles) and deep in the context.  The plan's share count is forced (EI_PREFILL_SPLIT,
+    read when the workspace is sized and at every call)."""
+    monkeypatch.setenv("EI_PREFILL_SPLIT", str(ksplit))
+    shape = gpu.AttnShape(H, HKV)
+    n = pos0 + B
+    k, v = _cache(orc, n, HKV, 190 + B + ksplit)
+    q = orc.normal((B, H * D), 191 + pos0)
+    ws = gpu.PrefillWorkspace(B, H, HKV, n)
+    assert ws.nbytes > 0, "the forced split must be planned"
+    out = _host(gpu.attn_prefill(_dev(q), _dev(k), _dev(v), _pos(pos0), shape, ws=ws))
+    ref = orc.attn_prefill(q, k, v, B, pos0, H, HKV, D)
+    kk, vv = k.reshape(n, -1), v.reshape(n, -1)
+    ok, msg = gate(f"prefill forced {ksplit} shares H{H}/HKV{HKV} B={B} pos0={pos0}", out, ref, lambda: np.stack(
+        [orc.attn_f64(q[b].reshape(H, D), kk, vv, pos0 + b + 1, H, HKV, D) for b in range(B)]))
+    assert ok, msg
+
+
+@pytest.mark.gpu
 def test_prefill_split_graph_replays_track_position(orc, gpu):
     """One captured split prefill replayed at three device positions (the plan is fixed by
     (B, max_kv)); each replay equals the reference at that position."""
