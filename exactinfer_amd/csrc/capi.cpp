@@ -295,6 +295,9 @@ int check_paged(const int* block_table, int max_blocks, int block_size, const in
             "block_size %d must be a power of two >= 16 (whole 16-key tiles per block)", block_size);
     REQUIRE(max_blocks > 0 && (long)max_blocks * block_size >= max_kv,
             "max_blocks %d x block_size %d does not cover max_kv %d", max_blocks, block_size, max_kv);
+    // the kernels index a sequence's keys and the table's span with 32-bit ints
+    REQUIRE((long)max_blocks * block_size <= 0x7FFFFFFFL, "max_blocks %d x block_size %d exceeds 2^31 - 1 keys",
+            max_blocks, block_size);
     REQUIRE(max_kv > 0 && (long)max_kv <= (long)ei::kDecodeMaxSplits * ei::kDecodePagedMaxChunk,
             "max_kv %d out of range for paged decode", max_kv);
     int sh = 0;
@@ -470,6 +473,9 @@ EI_API int ei_prefill_step_paged(ei_stream_t stream, float* qkv, long row_stride
             "block_size %d must be a power of two >= 32 (whole 32-key prefill tiles per block)", block_size);
     REQUIRE(max_blocks > 0 && (long)max_blocks * block_size >= max_kv,
             "max_blocks %d x block_size %d does not cover max_kv %d", max_blocks, block_size, max_kv);
+    // the kernels index a sequence's keys and the table's span with 32-bit ints
+    REQUIRE((long)max_blocks * block_size <= 0x7FFFFFFFL, "max_blocks %d x block_size %d exceeds 2^31 - 1 keys",
+            max_blocks, block_size);
     int shift = 0;
     while ((1 << shift) < block_size) ++shift;
     return prefill_step_impl(stream, qkv, row_stride, out, kc, vc, pos_dev, B, n_head, n_head_kv, head_dim, q_gamma,

@@ -127,6 +127,9 @@ def test_paged_argument_errors():
         _capi.call("ei_attn_decode_paged", None, p, 4096, p, p, p, p, 4, 16, p, 2, 32, 8, 128, 0.1, 128, p, 1 << 20)
     with pytest.raises(_capi.EiError, match="block_table and kv_len"):
         _capi.call("ei_attn_decode_paged", None, p, 4096, p, p, p, None, 8, 16, p, 2, 32, 8, 128, 0.1, 128, p, 1 << 20)
+    with pytest.raises(_capi.EiError, match="exceeds 2"):  # a table spanning more keys than 32-bit indices reach
+        _capi.call("ei_attn_decode_paged", None, p, 4096, p, p, p, p, 1 << 26, 64, p, 2, 32, 8, 128, 0.1, 128, p,
+                   1 << 20)
 
 
 def test_fused_decode_rope_dim_multiple_of_4():
