@@ -104,6 +104,8 @@ def test_configs4_full_size_fused_step(orc, gpu, paged):
         assert ok, msg
     # the appended rows are the only change to the pool, bit for bit
     assert bits_equal(kh, k_host) and bits_equal(vh, v_host)
+    # the plan splits the long sequences into 1024-key chunks merged inside the launch
+    assert ws.status() == 0, "a workgroup ran off the XCD placement the merge relies on"
 
 
 def test_configs2_prefill_step_full_size(orc, gpu):
