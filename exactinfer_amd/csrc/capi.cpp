@@ -150,11 +150,11 @@ EI_API int ei_attn_workspace_init(ei_stream_t stream, void* ws, size_t ws_bytes)
 namespace {
 
 int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void* ws, size_t ws_bytes, bool fused,
-                  bool launch_combine = false) {
+                  bool launch_combine = false, bool capped = true) {
     REQUIRE(max_kv > 0, "max_kv %d must be positive", max_kv);
     REQUIRE(ws != nullptr && aligned16(ws), "workspace missing or not 16-byte aligned");
-    const ei::DecodePlan p = ei::decode_plan(n_seq, a.HKV, max_kv, a.block_table != nullptr);
-    const ei::DecodeWsLayout lay = ei::decode_ws_layout(n_seq, a.H, a.HKV, max_kv);
+    const ei::DecodePlan p = ei::decode_plan(n_seq, a.HKV, max_kv, a.block_table != nullptr, capped);
+    const ei::DecodeWsLayout lay = ei::decode_ws_layout(n_seq, a.H, a.HKV, max_kv, capped);
     REQUIRE(ei::ws_fits(ws_bytes, lay.partials, lay.units),
             "workspace of %zu bytes too small for n_seq %d, max_kv %d (ei_attn_decode_ws_bytes gives %zu)", ws_bytes,
             n_seq, max_kv, ei::decode_ws_bytes(n_seq, a.H, a.HKV, max_kv));
@@ -251,20 +251,27 @@ int decode_step_impl(ei_stream_t stream, const float* qkv, long row_stride, floa
     a.cs = reinterpret_cast<const float2*>(cs);
     a.rope_dim = rope_dim;
     a.eps = eps;
+    bool capped = true;
     if (no_alloc) {
+        // the capped plan (1024-key chunks) if its partials fit the static array, else the plan
+        // without the cap (fewer splits of longer sequences: a ragged batch balances less well)
         REQUIRE(max_kv > 0, "max_kv %d must be positive", max_kv);
-        const ei::DecodeWsLayout lay = ei::decode_ws_layout(n_seq, n_head, n_head_kv, max_kv);
-        const size_t need = ei::decode_ws_bytes(n_seq, n_head, n_head_kv, max_kv);
-        REQUIRE(ei::ws_fits(ei::kDecodeScratchBytes, lay.partials, lay.units),
-                "n_seq %d, n_head %d, n_head_kv %d, max_kv %d need %zu bytes of scratch; the allocation-free step has "
-                "%zu (use ei_decode_step with a workspace)",
-                n_seq, n_head, n_head_kv, max_kv, need, ei::kDecodeScratchBytes);
+        const ei::DecodeWsLayout lay = ei::decode_ws_layout(n_seq, n_head, n_head_kv, max_kv, true);
+        if (!ei::ws_fits(ei::kDecodeScratchBytes, lay.partials, lay.units)) {
+            capped = false;
+            const ei::DecodeWsLayout lay2 = ei::decode_ws_layout(n_seq, n_head, n_head_kv, max_kv, false);
+            REQUIRE(ei::ws_fits(ei::kDecodeScratchBytes, lay2.partials, lay2.units),
+                    "n_seq %d, n_head %d, n_head_kv %d, max_kv %d need %zu bytes of scratch; the allocation-free step "
+                    "has %zu (use ei_decode_step with a workspace)",
+                    n_seq, n_head, n_head_kv, max_kv, ei::ws_bytes_for(lay2.partials, lay2.units),
+                    ei::kDecodeScratchBytes);
+        }
         if (int e = hip_status(ei::decode_scratch(&ws), "scratch address lookup")) return e;
         ws_bytes = ei::kDecodeScratchBytes;
     }
     // the allocation-free step always merges the splits in the second launch: its partials are
     // fully rewritten by every call, so nothing in the shared scratch has to start at zero
-    return decode_common(static_cast<hipStream_t>(stream), a, n_seq, max_kv, ws, ws_bytes, true, no_alloc);
+    return decode_common(static_cast<hipStream_t>(stream), a, n_seq, max_kv, ws, ws_bytes, true, no_alloc, capped);
 }
 
 }  // namespace

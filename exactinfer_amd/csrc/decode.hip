@@ -752,7 +752,7 @@ static int pow2_ceil(long x) {
     return p;
 }
 
-DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged) {
+DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged, bool capped) {
     // Keys are split as far as it takes to reach about one workgroup per CU (256): chunk =
     // max_kv / ceil(256 / (n_seq * HKV)), rounded up to a power of two >= 128 (128 fills every
     // wave's two-tile ring once), and at most 1024 keys: a batch of ragged sequences (the plan
@@ -765,7 +765,7 @@ DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged) {
     const long want = units >= 256 ? 1 : (256 + units - 1) / units;
     int chunk = pow2_ceil(((long)max_kv + want - 1) / want);
     if (chunk < 128) chunk = 128;
-    if (chunk > kDecodeMaxChunk) chunk = kDecodeMaxChunk;
+    if (capped && chunk > kDecodeMaxChunk) chunk = kDecodeMaxChunk;
     if (const char* env = std::getenv("EI_DECODE_CHUNK")) {  // tuning override (multiple of 64)
         const int v = std::atoi(env);
         if (v >= 64 && v % 64 == 0) chunk = v;
@@ -782,9 +782,10 @@ DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged) {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-DecodeWsLayout decode_ws_layout(int n_seq, int H, int HKV, int max_kv) {
+DecodeWsLayout decode_ws_layout(int n_seq, int H, int HKV, int max_kv, bool capped) {
     // sized for the larger of the paged and contiguous plans, so one workspace serves both
-    const DecodePlan p0 = decode_plan(n_seq, HKV, max_kv, false), p1 = decode_plan(n_seq, HKV, max_kv, true);
+    const DecodePlan p0 = decode_plan(n_seq, HKV, max_kv, false, capped);
+    const DecodePlan p1 = decode_plan(n_seq, HKV, max_kv, true, capped);
     const DecodePlan p = p0.nsplit >= p1.nsplit ? p0 : p1;
     const size_t slots = (size_t)n_seq * HKV * p.nsplit;
     const int G = decode_group_slots(H / HKV);

@@ -61,13 +61,15 @@ struct DecodePlan {
 constexpr int kDecodeMaxSplits = 256;
 constexpr int kDecodePagedMaxChunk = 8192;  // 4 waves x 128 tiles of 16 keys
 constexpr int kDecodeMaxChunk = 1024;       // longer keys are split (ragged batches balance across CUs)
-DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged);
+// capped: chunks of at most kDecodeMaxChunk keys (every workspace call); the allocation-free step
+// falls back to the uncapped plan when the capped one does not fit its static array
+DecodePlan decode_plan(int n_seq, int HKV, int max_kv, bool paged, bool capped = true);
 size_t decode_ws_bytes(int n_seq, int H, int HKV, int max_kv);
 // the call's partials: accumulators at 0, then the split records (ending at `partials`)
 struct DecodeWsLayout {
     size_t rec, partials, units;
 };
-DecodeWsLayout decode_ws_layout(int n_seq, int H, int HKV, int max_kv);
+DecodeWsLayout decode_ws_layout(int n_seq, int H, int HKV, int max_kv, bool capped = true);
 int decode_group_slots(int g);  // heads per KV head the decode kernel is built for (0: unsupported)
 
 struct DecodeArgs {

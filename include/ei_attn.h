@@ -141,7 +141,8 @@ int ei_attn_decode_batched(ei_stream_t stream, const float* q, long q_stride, fl
                            int n_head_kv, int head_dim, float scale, int max_kv, void* ws, size_t ws_bytes);
 
 /* Fused decode step: ei_qkv_prepare + ei_attn_decode for one token per sequence in one
- * decode launch (the split combine happens inside it; rope_dim must be a multiple of 4).  qkv row s (at qkv + s*row_stride, [Q|K|V] raw projections) is read only;
+ * decode launch (the splits of chunks over 128 keys merge inside it, shorter ones in a second
+ * small launch; rope_dim must be a multiple of 4).  qkv row s (at qkv + s*row_stride, [Q|K|V] raw projections) is read only;
  * the normed+roped K row and the V row are written to cache row kv_offset[s] + pos_s,
  * pos_s = kv_len[s]-1 (or *pos_dev when kv_len is NULL; then n_seq must be 1 and
  * kv_offset may be NULL).  out [n_seq][n_head][128].  Equivalent to the per-layer
@@ -155,12 +156,14 @@ int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride, float*
 /* Allocation-free fused decode step.  No counterpart in the reference: it is for callers that
  * cannot allocate or pass a workspace (code under HIP graph capture set up before any
  * workspace exists, tight serving loops, harnesses that forbid allocation).  Same arguments,
- * semantics and results as ei_decode_step without (ws, ws_bytes); the split partials live in a
- * static device array of 4 MiB per GPU, held until the process ends, so the call allocates
- * nothing.  A shape whose ei_attn_decode_ws_bytes(n_seq, n_head, n_head_kv, max_kv) exceeds
- * 4 MiB is rejected with EI_ERR_ARG (one sequence at H32/HKV8 takes 0.53 MiB up to max_kv
- * 32768; 64 sequences at H16/HKV8 take 0.56 MiB at max_kv 8192 and 4.5 MiB, too much, at
- * 65536; 256 sequences at H32/HKV8 and max_kv 4096 take 4.25 MiB, too much).  Every call on one GPU shares that array:
+ * semantics as ei_decode_step without (ws, ws_bytes); the split partials live in a static
+ * device array of 4 MiB per GPU, held until the process ends, so the call allocates nothing.
+ * It runs ei_decode_step's plan (chunks of at most 1024 keys) when that plan's partials fit the
+ * array, and otherwise the plan without the chunk cap (fewer, longer splits: results within the
+ * parity bar, bits may differ from ei_decode_step's); a shape that fits neither is rejected with
+ * EI_ERR_ARG.  One sequence at H32/HKV8 takes 0.57 MiB up to max_kv 32768; 64 sequences at
+ * H16/HKV8 and max_kv 8192 take 4.8 MiB capped (too much) and 0.56 MiB uncapped; 256 sequences
+ * at H32/HKV8 and max_kv 4096 take 4.25 MiB even uncapped (rejected).  Every call on one GPU shares that array:
  * calls that overlap in time on one GPU (two streams, two threads) race and must not be made.
  * The splits are always merged by the second small launch. */
 int ei_decode_step_noalloc(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc, float* vc,
@@ -171,8 +174,9 @@ int ei_decode_step_noalloc(ei_stream_t stream, const float* qkv, long row_stride
 /* ------------------------------------------------------------------ paged KV (multi-sequence serving)
  * Sequence s's key t lives in cache row block_table[s*max_blocks + t/block_size]*block_size
  * + t%block_size of the shared pool kc/vc (rows of n_head_kv*128 floats); block_size is a
- * power of two >= 16, max_blocks*block_size >= max_kv, 0 <= kv_len[s] <= max_kv (kv_len
- * 0 gives zeros).  Sequences may share physical blocks (a common prefix cached once).  The
+ * power of two >= 16, max_blocks*block_size >= max_kv and < 2^31, 0 <= kv_len[s] (kv_len 0
+ * gives zeros; a kv_len above max_kv is still attended in full, one beyond the table's span
+ * max_blocks*block_size, outside the contract, is read only up to that span and appends nothing).  Sequences may share physical blocks (a common prefix cached once).  The
  * reference decodes one contiguous sequence (src/cuda/model_cuda.cu:1043-1111); these are
  * the serve-side extension of ei_attn_decode_batched and ei_decode_step: per sequence the
  * result is that of ei_attn_decode on the gathered rows.  ei_decode_step_paged writes the

@@ -66,6 +66,46 @@ def test_noalloc_decode_step_matches_workspace_step(orc, gpu):
         assert bits_equal(_host(kc_a), _host(kc_b)) and bits_equal(_host(vc_a), _host(vc_b)), f"cache differs for {c}"
 
 
+def test_noalloc_falls_back_to_the_uncapped_plan(orc, gpu):
+    """64 sequences planned for 8192 keys: the workspace plan's 1024-key splits need 4.8 MiB, more
+    than the static array; the allocation-free step then runs the plan without the chunk cap (one
+    split per sequence and KV head).  Two calls in a row; each output within the parity gate of the
+    reference attention, the appended rows bit-identical to the workspace step's."""
+    import torch
+    from tests.parity import gate
+    from exactinfer_amd import _capi
+    H, HKV, max_kv, n_seq = 16, 8, 8192, 64
+    assert _capi.lib().ei_attn_decode_ws_bytes(n_seq, H, HKV, max_kv) > 4 << 20
+    shape = gpu.AttnShape(H, HKV)
+    for call, seed in enumerate((7200, 7300)):
+        rng = np.random.default_rng(seed)
+        lens = rng.integers(1, 600 if call == 0 else 200, n_seq).astype(np.int32)
+        offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+        rows = int(lens.sum())
+        k, v = orc.normal((rows, HKV * D), seed), orc.normal((rows, HKV * D), seed + 1)
+        qkv_h = orc.normal((n_seq, shape.qkv), seed + 2)
+        qg_h, kg_h = orc.gamma(D, seed + 3), orc.gamma(D, seed + 4)
+        qkv, qg, kg = _dev(qkv_h), _dev(qg_h), _dev(kg_h)
+        cs = gpu.rope_table(max_kv)
+        kc_a, vc_a, kc_b, vc_b = _dev(k), _dev(v), _dev(k), _dev(v)
+        od, ld = _dev(offs), _dev(lens)
+        out_a = torch.full((n_seq, H, D), float("nan"), device="cuda")
+        _noalloc(gpu, qkv, kc_a, vc_a, shape, qg, kg, cs, max_kv, out_a, kv_offset=od, kv_len=ld)
+        ws = gpu.DecodeWorkspace(n_seq, H, HKV, max_kv)
+        gpu.decode_step(qkv, kc_b, vc_b, shape, qg, kg, cs, ws, kv_offset=od, kv_len=ld)
+        ka, va = _host(kc_a), _host(vc_a)
+        assert bits_equal(ka, _host(kc_b)) and bits_equal(va, _host(vc_b)), f"call {call}: appended rows differ"
+        got = _host(out_a)
+        for s_ in range(n_seq):
+            n, o = int(lens[s_]), int(offs[s_])
+            normed = orc.headnorm_rope(qkv_h[s_:s_ + 1], H, D, qg_h, n - 1, 128, 1e6, 1e-6)
+            qn = np.ascontiguousarray(normed[0, :H * D].reshape(H, D))
+            kk, vv = ka[o:o + n].reshape(n, HKV, D), va[o:o + n].reshape(n, HKV, D)
+            ok, msg = gate(f"noalloc uncapped call {call} seq {s_} len {n}", got[s_],
+                           orc.attn_decode(qn, kk, vv, n, H, HKV, D), lambda: orc.attn_f64(qn, kk, vv, n, H, HKV, D))
+            assert ok, msg
+
+
 def test_noalloc_rejects_shapes_beyond_its_scratch(gpu):
     from exactinfer_amd import _capi
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
