@@ -7,7 +7,8 @@
  *
  * Build: gcc -O2 -ffp-contract=off (no contraction, no reassociation) so every float
  * operation happens in the order the reference writes it (MSVC /fp:precise semantics of
- * the reference build, CMakeLists.txt:49).  OpenMP only splits independent query heads,
+ * the reference build, CMakeLists.txt:49), with that build's ISA (-mavx2 -mfma -mf16c for
+ * its /arch:AVX2), which changes no result under those two rules.  OpenMP only splits independent query heads,
  * exactly like the reference (src/model.cpp:191), so results do not depend on thread count.
  *
  * Pinning of each function (what proves the restatement right, checked in tests/):
