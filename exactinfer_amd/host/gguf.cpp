@@ -305,7 +305,8 @@ Qwen3Config qwen3_config(const GgufFile& g) {
     c.n_ff = static_cast<int>(g.get_int(p + "feed_forward_length"));
     c.n_head = static_cast<int>(g.get_int(p + "attention.head_count"));
     c.n_head_kv = static_cast<int>(g.get_int_or(p + "attention.head_count_kv", c.n_head));
-    c.head_dim = static_cast<int>(g.get_int_or(p + "attention.key_length", c.n_head ? c.n_embd / c.n_head : 0));
+    // (a head count <= 0 is rejected below either way; dividing by it is not attempted)
+    c.head_dim = static_cast<int>(g.get_int_or(p + "attention.key_length", c.n_head > 0 ? c.n_embd / c.n_head : 0));
     if (g.get_int_or(p + "attention.value_length", c.head_dim) != c.head_dim)
         throw std::runtime_error("key_length != value_length is not supported");
     c.rope_dim = static_cast<int>(g.get_int_or(p + "rope.dimension_count", c.head_dim));

@@ -21,7 +21,7 @@ ROOT = Path(__file__).resolve().parent.parent.parent
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
-T_U32, T_I32, T_F32, T_STRING, T_U64, T_F64 = 4, 5, 6, 8, 10, 12
+T_U32, T_I32, T_F32, T_STRING, T_ARRAY, T_U64, T_F64 = 4, 5, 6, 8, 9, 10, 12
 
 
 def _s(x: str) -> bytes:
@@ -29,12 +29,18 @@ def _s(x: str) -> bytes:
     return struct.pack("<Q", len(b)) + b
 
 
-def _kv(key: str, t: int, value) -> bytes:
-    out = _s(key) + struct.pack("<I", t)
+def _val(t: int, value) -> bytes:
     if t == T_STRING:
-        return out + _s(value)
+        return _s(value)
+    if t == T_ARRAY:  # value = (element type, list of elements)
+        et, items = value
+        return struct.pack("<IQ", et, len(items)) + b"".join(_val(et, x) for x in items)
     fmt = {T_U32: "<I", T_I32: "<i", T_F32: "<f", T_U64: "<Q", T_F64: "<d"}[t]
-    return out + struct.pack(fmt, value)
+    return struct.pack(fmt, value)
+
+
+def _kv(key: str, t: int, value) -> bytes:
+    return _s(key) + struct.pack("<I", t) + _val(t, value)
 
 
 def quantize_q8_0(a: np.ndarray) -> np.ndarray:

@@ -7,12 +7,16 @@ validation (read_config / read_tensors, src/model.cpp:38-103); and every class o
 the reference reader rejects (src/gguf.cpp:203-254): truncation anywhere, wrong magic or version,
 implausible counts, bad dimensions or types, repeated keys or names, bad alignment, tensors
 misaligned or past the end.  The forward pass of the model read back equals the in-memory one."""
+import shutil
 import struct
+import subprocess
+from pathlib import Path
 
 import numpy as np
 import pytest
 
-from tests.golden.write_tiny_gguf import T_STRING, T_U32, Quantised, qwen3_metadata, qwen3_tensors, write_gguf
+from tests.golden.write_tiny_gguf import (T_ARRAY, T_F32, T_I32, T_STRING, T_U32, Quantised, qwen3_metadata,
+                                         qwen3_tensors, write_gguf)
 from tests.tiny_qwen3 import TinyQwen3, oracle_attention, run_sequence
 
 
@@ -44,13 +48,21 @@ def _parse_independently(path):
         at[0] += n
         return s
 
+    def rv(t):
+        if t == T_STRING:
+            return rs()
+        if t == T_ARRAY:
+            et, n = rd("<I"), rd("<Q")
+            return [rv(et) for _ in range(n)]
+        return rd({4: "<I", 6: "<f", 5: "<i", 10: "<Q", 12: "<d"}[t])
+
     assert rd("<I") == 0x46554747
     rd("<I")
     nt, nkv = rd("<Q"), rd("<Q")
     meta = {}
     for _ in range(nkv):
         k, t = rs(), rd("<I")
-        meta[k] = rs() if t == T_STRING else rd({4: "<I", 6: "<f", 5: "<i", 10: "<Q", 12: "<d"}[t])
+        meta[k] = rv(t)
     tensors = {}
     for _ in range(nt):
         name, nd = rs(), rd("<I")
@@ -282,3 +294,45 @@ def test_k_quant_attention_weights_round_trip(tmp_path, orc, attn_type, tid, rel
     assert np.corrcoef(dq.ravel(), w.ravel())[0, 1] >= 0.995
     model = TinyQwen3.from_gguf(p, dequant=orc.dequant)
     assert np.array_equal(model.layers[0]["wqkv"][:4 * 128], dq)
+
+
+def _fuzz_seeds(tmp_path):
+    """Small files of each shape the reader meets: F16 matrices with tokenizer arrays in the
+    metadata (string, float and integer arrays), F32 with Q8_0 attention projections, and a
+    version-2 file aligned to 64 bytes."""
+    m = TinyQwen3(seed=11, n_layer=2, n_embd=32, n_head=2, n_head_kv=1, n_ff=32, n_vocab=8)
+    toks = [("tokenizer.ggml.model", T_STRING, "gpt2"),
+            ("tokenizer.ggml.tokens", T_ARRAY, (T_STRING, [f"t{i}" for i in range(8)])),
+            ("tokenizer.ggml.scores", T_ARRAY, (T_F32, [float(-i) for i in range(8)])),
+            ("tokenizer.ggml.token_type", T_ARRAY, (T_I32, [1] * 8))]
+    seeds = [tmp_path / "f16.gguf", tmp_path / "q8.gguf", tmp_path / "v2.gguf"]
+    write_gguf(seeds[0], qwen3_metadata(m) + toks, qwen3_tensors(m, True))
+    write_gguf(seeds[1], qwen3_metadata(m), qwen3_tensors(m, False, attn_type="q8_0"))
+    write_gguf(seeds[2], qwen3_metadata(m, alignment=64), qwen3_tensors(m, True), alignment=64, version=2)
+    return seeds
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ builds the sanitizer-instrumented harness")
+def test_mutated_files_under_sanitizers(tmp_path):
+    """The reader and the Qwen3 checks built with AddressSanitizer and UndefinedBehaviorSanitizer
+    (tests/cpp/gguf_fuzz.cpp) open 24 000 mutated copies of three small files (fixed seeds; three
+    mutations in four hit the header, metadata and tensor table): every file is either rejected
+    with the reader's error or read whole, every tensor view of an accepted file is read, and no
+    sanitizer report, crash, leak or other exception occurs."""
+    from exactinfer_amd.gguf import GgufFile
+    here = Path(__file__).resolve().parent
+    exe = tmp_path / "gguf_fuzz"
+    build = subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined",
+                            "-fno-sanitize-recover=all", "-fno-omit-frame-pointer", str(here / "cpp" / "gguf_fuzz.cpp"),
+                            str(here.parent / "exactinfer_amd" / "host" / "gguf.cpp"), "-o", str(exe)],
+                           capture_output=True, text=True)
+    assert build.returncode == 0, build.stderr
+    for i, seed in enumerate(_fuzz_seeds(tmp_path)):
+        with GgufFile(seed) as g:  # the seed itself is a valid file
+            g.qwen3_config()
+        header = _parse_independently(seed)[2]
+        r = subprocess.run([str(exe), str(seed), "8000", str(1000 + i), str(tmp_path / "scratch.gguf"), str(header)],
+                           capture_output=True, text=True, timeout=300)
+        assert r.returncode == 0, f"{seed.name}: {r.stderr[-3000:]}"
+        ok, accepted, rejected = r.stdout.split()[-3:]
+        assert ok == "ok" and int(accepted) > 0 and int(rejected) > 0, r.stdout[-200:]
