@@ -45,11 +45,19 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
         if (!(cond)) return fail(EI_ERR_ARG, __VA_ARGS__); \
     } while (0)
 
+// Shape limits that keep every size and index computation in range: KV heads per layer, and the
+// rows of one prefill chunk (B * n_head query rows, B <= 2^20 tokens).
+constexpr int kMaxKvHeads = 1024;
+constexpr long kMaxPrefillB = 1L << 20, kMaxPrefillRows = 1L << 28;
+
+bool prefill_rows_ok(int B, int n_head) { return B <= kMaxPrefillB && (long)B * n_head <= kMaxPrefillRows; }
+
 int check_heads(int n_head, int n_head_kv, int head_dim) {
     if (head_dim != 128)
         return fail(EI_ERR_UNSUPPORTED, "head_dim %d: only 128 is built (the reference GPU path requires it too)",
                     head_dim);
     REQUIRE(n_head > 0 && n_head_kv > 0, "n_head (%d) and n_head_kv (%d) must be positive", n_head, n_head_kv);
+    REQUIRE(n_head_kv <= kMaxKvHeads, "n_head_kv %d above %d", n_head_kv, kMaxKvHeads);
     REQUIRE(n_head % n_head_kv == 0, "n_head %d is not a multiple of n_head_kv %d", n_head, n_head_kv);
     const int g = n_head / n_head_kv;
     if (g > 8) return fail(EI_ERR_UNSUPPORTED, "GQA group %d: built for groups of 1 to 8 query heads", g);
@@ -137,7 +145,9 @@ EI_API int ei_qkv_prepare(ei_stream_t stream, float* qkv, int rows, long row_str
 }
 
 EI_API size_t ei_attn_decode_ws_bytes(int n_seq, int n_head, int n_head_kv, int max_kv) {
-    if (n_seq <= 0 || n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv || max_kv <= 0) return 0;
+    if (n_seq <= 0 || n_seq > 65535 || n_head <= 0 || n_head_kv <= 0 || n_head_kv > kMaxKvHeads || n_head % n_head_kv ||
+        max_kv <= 0)
+        return 0;
     return ei::decode_ws_bytes(n_seq, n_head, n_head_kv, max_kv);
 }
 
@@ -169,6 +179,8 @@ int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void
     a.nsplit = p.nsplit;
     a.units = n_seq * a.HKV;
     a.n_xcc = ei::device_xccs();
+    REQUIRE(((long)a.units + a.n_xcc) * a.nsplit <= 0x7FFFFFFFL,
+            "n_seq %d x n_head_kv %d x %d key splits: more workgroups than one launch takes", n_seq, a.HKV, a.nsplit);
     a.merge_in_kernel = !launch_combine && ei::decode_merge_in_kernel(p.chunk);
     return hip_status(ei::launch_decode(st, a, n_seq, fused), "decode launch");
 }
@@ -384,6 +396,8 @@ EI_API int ei_attn_prefill(ei_stream_t stream, const float* q, long q_stride, fl
     if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
     REQUIRE(q && out && kc && vc && pos_dev, "null pointer argument");
     REQUIRE(B >= 0, "B %d", B);
+    REQUIRE(prefill_rows_ok(B, n_head), "B %d x n_head %d: at most 2^20 tokens and 2^28 query rows per launch", B,
+            n_head);
     REQUIRE(q_stride >= (long)n_head * head_dim && q_stride % 4 == 0, "q_stride %ld", q_stride);
     REQUIRE(aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc), "pointers must be 16-byte aligned");
     if (B == 0) return ok();
@@ -394,6 +408,7 @@ EI_API int ei_attn_prefill(ei_stream_t stream, const float* q, long q_stride, fl
 
 EI_API size_t ei_attn_prefill_ws_bytes(int max_B, int n_head, int n_head_kv, int max_kv) {
     if (max_B <= 0 || n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv || max_kv < max_B) return 0;
+    if (n_head_kv > kMaxKvHeads || !prefill_rows_ok(max_B, n_head)) return 0;
     size_t most = 0;  // the plan varies with B: size for every chunk of up to max_B rows
     for (int b = 1; b <= max_B; ++b) {
         const size_t need = ei::prefill_ws_bytes(b, n_head, n_head_kv, max_kv);
@@ -408,6 +423,8 @@ EI_API int ei_attn_prefill_split(ei_stream_t stream, const float* q, long q_stri
     if (int e = check_heads(n_head, n_head_kv, head_dim)) return e;
     REQUIRE(q && out && kc && vc && pos_dev, "null pointer argument");
     REQUIRE(B >= 0, "B %d", B);
+    REQUIRE(prefill_rows_ok(B, n_head), "B %d x n_head %d: at most 2^20 tokens and 2^28 query rows per launch", B,
+            n_head);
     REQUIRE(max_kv >= B, "max_kv %d < B %d", max_kv, B);
     REQUIRE(q_stride >= (long)n_head * head_dim && q_stride % 4 == 0, "q_stride %ld", q_stride);
     REQUIRE(aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc), "pointers must be 16-byte aligned");
@@ -431,6 +448,8 @@ int prefill_step_impl(ei_stream_t stream, float* qkv, long row_stride, float* ou
     if (int e = check_rope(rope_dim, head_dim)) return e;
     REQUIRE(qkv && out && kc && vc && pos_dev && q_gamma && k_gamma && cs, "null pointer argument");
     REQUIRE(B >= 0, "B %d", B);
+    REQUIRE(prefill_rows_ok(B, n_head), "B %d x n_head %d: at most 2^20 tokens and 2^28 query rows per launch", B,
+            n_head);
     REQUIRE(max_kv >= B, "max_kv %d < B %d", max_kv, B);
     REQUIRE(row_stride >= (long)(n_head + 2 * n_head_kv) * head_dim, "row_stride %ld < (H+2*HKV)*head_dim",
             row_stride);

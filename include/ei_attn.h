@@ -16,6 +16,9 @@
  *    src/cuda/model_cuda.cu:46, :1542); n_head must be a multiple of n_head_kv with a
  *    group size of 1 to 8 (every dense Qwen3: 0.6B-8B and 32B have 2, 4 or 8, 14B has 5);
  *    rope_dim even and <= head_dim.
+ *  - Shape limits that keep sizes and indices in range (EI_ERR_ARG past them; the workspace
+ *    size queries return 0): n_head_kv <= 1024; decode batches of at most 65535 sequences and
+ *    2^31 workgroups; prefill chunks of at most 2^20 tokens and 2^28 (token, query head) rows.
  *  - KV cache layout per layer: [position][n_head_kv][head_dim] fp32 (src/model.cpp:153,
  *    src/cuda/model_cuda.cu:1571), i.e. row p holds kd = n_head_kv*128 floats.
  *  - Base pointers and row strides must be 16-byte aligned (multiples of 4 floats).

@@ -59,6 +59,28 @@ def test_argument_errors_are_reported_not_thrown():
     assert "rope_dim" in _capi.last_error()
 
 
+def test_shape_limits_are_reported():
+    """Shapes past what the size and index arithmetic holds are rejected, not wrapped: more than 1024
+    KV heads, prefill chunks past 2^20 tokens or 2^28 query rows, decode grids past 2^31 workgroups;
+    the size queries return 0 for them."""
+    from exactinfer_amd import _capi
+    L = _capi.lib()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    with pytest.raises(_capi.EiError, match="n_head_kv 2048 above 1024"):
+        _capi.call("ei_attn_prefill", None, p, 1 << 22, p, p, p, p, 8, 4096, 2048, 128, 0.1)
+    assert L.ei_attn_decode_ws_bytes(1, 4096, 2048, 4096) == 0
+    assert L.ei_attn_decode_ws_bytes(65536, 32, 8, 4096) == 0
+    with pytest.raises(_capi.EiError, match="2\\^20 tokens"):
+        _capi.call("ei_attn_prefill", None, p, 4096, p, p, p, p, (1 << 20) + 1, 32, 8, 128, 0.1)
+    with pytest.raises(_capi.EiError, match="2\\^28 query rows"):
+        _capi.call("ei_attn_prefill_split", None, p, 1 << 20, p, p, p, p, 1 << 20, 512, 64, 128, 0.1, 1 << 20, p,
+                   1 << 40)
+    assert L.ei_attn_prefill_ws_bytes(1 << 20, 512, 64, 1 << 20) == 0
+    with pytest.raises(_capi.EiError, match="more workgroups than one launch takes"):
+        _capi.call("ei_attn_decode_batched", None, p, 1 << 20, p, p, p, p, p, 65535, 8192, 1024, 128, 0.1, 1 << 20,
+                   p, 1 << 50)
+
+
 def test_decode_workspace_size_is_monotone():
     from exactinfer_amd import _capi
     L = _capi.lib()
