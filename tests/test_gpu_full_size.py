@@ -7,6 +7,7 @@
   q-norm-in-kernel plan), sampled rows against the reference, the whole cache bit-exact.
 - The in-kernel split merge (chunks over 128 keys): consecutive calls and graph replays, where
   every launch advances the split records' epoch.
+- A 512-token chunk at position 32256 of a 32768-row context (8 key shares), contiguous and paged.
 - Edge contracts: a kv_len beyond the workspace's max_kv, and a fused decode with rope_dim 64.
 Calls go through the C ABI; the reference is the oracle's restatement of src/model.cpp:191-214
 (oracle/oracle.c), QK-norm + RoPE of src/ops.cpp:155-160 and src/model.cpp:23-32.
@@ -130,6 +131,53 @@ def test_configs2_prefill_step_full_size(orc, gpu):
         q = np.ascontiguousarray(normed[b, :H * D].reshape(H, D))
         ref = orc.attn_decode(q, kk, vv, b + 1, H, HKV, D)
         ok, msg = gate(f"configs[2] prefill step row {b}", out[b], ref, lambda: orc.attn_f64(q, kk, vv, b + 1, H, HKV, D))
+        assert ok, msg
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_long_position_prefill_chunk(orc, gpu, paged):
+    """A 512-token chunk at the end of a 32768-row context (configs[3]'s H16/HKV8): the plan cuts each
+    unit pair's ~2000 key tiles into 8 shares (the most it makes), so the step takes the full
+    prologue and the share combine reads up to three shares per row.  Contiguous and on a paged
+    pool of shuffled 64-row blocks; the appended rows bit-exact, sampled rows (both ends of each
+    32-row block among them) against the reference."""
+    H, HKV, B, bs = 16, 8, 512, 64
+    n_ctx = 32768
+    pos0 = n_ctx - B
+    shape = gpu.AttnShape(H, HKV)
+    kd = HKV * D
+    assert gpu._capi.lib().ei_attn_prefill_ws_bytes(B, H, HKV, n_ctx) >= 8 * B * H * D * 4  # 8 shares
+    k, v = orc.normal((n_ctx, kd), 2600), orc.normal((n_ctx, kd), 2601)
+    qkv = orc.normal((B, shape.qkv), 2602)
+    qg, kg = orc.gamma(D, 2603), orc.gamma(D, 2604)
+    cs = gpu.rope_table(n_ctx)
+    ws = gpu.PrefillWorkspace(B, H, HKV, n_ctx)
+    if paged:
+        rng = np.random.default_rng(2605)
+        nblk = n_ctx // bs
+        table = rng.permutation(nblk).astype(np.int32)
+        rows = (table[np.arange(n_ctx) // bs].astype(np.int64) * bs + np.arange(n_ctx) % bs)
+        pk, pv = np.empty_like(k), np.empty_like(v)
+        pk[rows], pv[rows] = k, v
+        kc, vc = _dev(pk), _dev(pv)
+        out = _host(gpu.prefill_step(_dev(qkv), kc, vc, shape, _dev(qg), _dev(kg), cs, _pos(pos0), ws,
+                                     block_table=_dev(table), block_size=bs))
+        kc_h, vc_h = _host(kc)[rows], _host(vc)[rows]
+    else:
+        kc, vc = _dev(k), _dev(v)
+        out = _host(gpu.prefill_step(_dev(qkv), kc, vc, shape, _dev(qg), _dev(kg), cs, _pos(pos0), ws))
+        kc_h, vc_h = _host(kc), _host(vc)
+    normed = orc.headnorm_rope(qkv, H, D, qg, pos0, 128, 1e6, 1e-6)
+    normed = orc.headnorm_rope(normed, HKV, D, kg, pos0, 128, 1e6, 1e-6, col0=H * D)
+    rk, rv = k.copy(), v.copy()
+    orc.kv_append(normed[:, H * D:(H + HKV) * D], normed[:, (H + HKV) * D:], rk, rv, pos0)
+    assert bits_equal(kc_h, rk) and bits_equal(vc_h, rv)
+    kk, vv = rk.reshape(n_ctx, HKV, D), rv.reshape(n_ctx, HKV, D)
+    for b in (0, 1, 31, 32, 255, 256, 480, 511):
+        q = np.ascontiguousarray(normed[b, :H * D].reshape(H, D))
+        ref = orc.attn_decode(q, kk, vv, pos0 + b + 1, H, HKV, D)
+        ok, msg = gate(f"long-position chunk {'paged' if paged else 'contiguous'} row {b}", out[b], ref,
+                       lambda: orc.attn_f64(q, kk, vv, pos0 + b + 1, H, HKV, D))
         assert ok, msg
 
 
