@@ -16,7 +16,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libei_attn.so"
 SOURCES = ["csrc/prologue.hip", "csrc/decode.hip", "csrc/prefill.hip", "csrc/project.hip", "csrc/capi.cpp",
-           "host/hip_attention.cpp", "host/gguf.cpp"]
+           "host/hip_attention.cpp", "host/gguf_index.cpp", "host/qwen3_schema.cpp"]
 HEADERS = ["common.h", "launch.h"]
 
 HIPCC_FLAGS = [
@@ -54,7 +54,7 @@ def build(verbose: bool = False) -> Path:
 
 def inputs() -> list[Path]:
     """Every file the library is built from: the sources, the private headers and the ABI header."""
-    return ([PKG / s for s in SOURCES] + [CSRC / h for h in HEADERS] + [PKG / "host" / h for h in ("gguf.h", "hip_attention.h")] +
+    return ([PKG / s for s in SOURCES] + [CSRC / h for h in HEADERS] + [PKG / "host" / h for h in ("gguf_index.h", "hip_attention.h")] +
             [ROOT / "include" / h for h in ("ei_attn.h", "ei_gguf.h")])
 
 

@@ -11,7 +11,7 @@
 
 #include "../../include/ei_attn.h"
 #include "../../include/ei_gguf.h"
-#include "../host/gguf.h"
+#include "../host/gguf_index.h"
 #include "launch.h"
 
 namespace {
@@ -553,7 +553,7 @@ EI_API int ei_synth_fill(ei_stream_t stream, float* dst, size_t n, uint64_t seed
 
 // ------------------------------------------------------------------ GGUF reader (include/ei_gguf.h)
 struct ei_gguf {
-    ei::GgufFile file;
+    ei::gguf::Index file;
     explicit ei_gguf(const char* path) : file(path) {}
 };
 
@@ -584,20 +584,20 @@ EI_API int ei_gguf_tensor(const ei_gguf* g, long index, const char** name, int* 
                           const void** data, uint64_t* nbytes) {
     REQUIRE(g != nullptr, "file handle is null");
     REQUIRE(index >= 0 && index < (long)g->file.tensors().size(), "tensor index %ld out of range", index);
-    const ei::GgufTensor& t = g->file.tensors()[(size_t)index];
+    const ei::gguf::TensorSlot& t = g->file.tensors()[(size_t)index];
     if (name) *name = t.name.c_str();
     if (type) *type = (int)t.type;
-    if (n_dims) *n_dims = (int)t.ne.size();
+    if (n_dims) *n_dims = (int)t.rank;
     if (ne)
-        for (size_t i = 0; i < 4; ++i) ne[i] = i < t.ne.size() ? t.ne[i] : 1;
+        for (size_t i = 0; i < 4; ++i) ne[i] = t.dims[i];
     if (data) *data = t.data;
-    if (nbytes) *nbytes = t.nbytes;
+    if (nbytes) *nbytes = t.bytes;
     return ok();
 }
 
 EI_API long ei_gguf_find_tensor(const ei_gguf* g, const char* name) {
     if (!g || !name) return -1;
-    const ei::GgufTensor* t = g->file.tensor(name);
+    const ei::gguf::TensorSlot* t = g->file.tensor(name);
     return t ? (long)(t - g->file.tensors().data()) : -1;
 }
 
@@ -618,21 +618,21 @@ int gguf_call(const ei_gguf* g, const char* key, F f) {
 
 EI_API int ei_gguf_get_int(const ei_gguf* g, const char* key, int64_t* out) {
     return gguf_call(g, key, [&] {
-        const int64_t v = g->file.get_int(key);
+        const int64_t v = g->file.integer(key);
         if (out) *out = v;
     });
 }
 
 EI_API int ei_gguf_get_float(const ei_gguf* g, const char* key, double* out) {
     return gguf_call(g, key, [&] {
-        const double v = g->file.get_float(key);
+        const double v = g->file.number(key);
         if (out) *out = v;
     });
 }
 
 EI_API int ei_gguf_get_str(const ei_gguf* g, const char* key, const char** out) {
     return gguf_call(g, key, [&] {
-        const std::string& v = g->file.get_str(key);
+        const std::string& v = g->file.text(key);
         if (out) *out = v.c_str();
     });
 }
@@ -640,8 +640,7 @@ EI_API int ei_gguf_get_str(const ei_gguf* g, const char* key, const char** out) 
 EI_API int ei_gguf_qwen3_config(const ei_gguf* g, ei_qwen3_config* out) {
     REQUIRE(g != nullptr && out != nullptr, "null argument");
     try {
-        ei::Qwen3Config c = ei::qwen3_config(g->file);
-        (void)ei::qwen3_tensors(g->file, c);
+        const ei::gguf::Qwen3Config c = ei::gguf::qwen3_config(g->file);
         out->n_layer = c.n_layer;
         out->n_embd = c.n_embd;
         out->n_ff = c.n_ff;

@@ -1,4 +1,4 @@
-"""Python view of the GGUF reader (include/ei_gguf.h; exactinfer_amd/host/gguf.cpp).
+"""Python view of the GGUF reader (include/ei_gguf.h; exactinfer_amd/host/gguf_index.cpp).
 
 The C++ reader maps and validates the file; this module only wraps its C ABI: metadata by key,
 the tensor table, tensors as numpy arrays (copied out of the mapping, so they outlive the file),

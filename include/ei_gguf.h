@@ -1,6 +1,7 @@
 /*
- * ei_gguf.h — C ABI of the GGUF model-file reader (exactinfer_amd/host/gguf.{h,cpp}) in
- * libei_attn.so: the Qwen3 weights the attention path's callers feed it come from these files.
+ * ei_gguf.h — C ABI of the GGUF model-file reader in libei_attn.so
+ * (exactinfer_amd/host/gguf_index.{h,cpp}, qwen3_schema.cpp): the Qwen3 weights the attention
+ * path's callers feed it come from these files.
  *
  * Replaces the reference's el::Gguf (src/gguf.h:55-84, src/gguf.cpp:203-306; Win32-only there)
  * and read_config / read_tensors (src/model.cpp:38-103).  Conventions are those of ei_attn.h:

@@ -1,5 +1,5 @@
-// gguf_fuzz.cpp — mutation test of the GGUF reader (exactinfer_amd/host/gguf.cpp), built with
-// AddressSanitizer and UndefinedBehaviorSanitizer by tests/test_gguf.py.
+// gguf_fuzz.cpp — mutation test of the GGUF reader (exactinfer_amd/host/gguf_index.cpp and
+// qwen3_schema.cpp), built with AddressSanitizer and UndefinedBehaviorSanitizer by tests/test_gguf.py.
 //
 // usage: gguf_fuzz <seed file> <iterations> <rng seed> <scratch path> <header bytes>
 //
@@ -7,10 +7,10 @@
 // 8- or 4-byte field overwritten with a boundary value, a truncation, a copied span), writes it
 // to the scratch path and opens it.  Three mutations in four land in the first <header bytes>
 // (the header, metadata and tensor table), the rest anywhere.  A file must either be rejected
-// with GgufError (or, past the reader, with the runtime_error of the Qwen3 checks) or be read
+// with the reader's FormatError (from the index or from the Qwen3 checks) or be read
 // whole: every tensor's bytes are then summed, which touches each view the reader handed out.  Any other exception, a crash
 // or a sanitizer report fails the run.  The last line is "ok <accepted> <rejected>".
-#include "../../exactinfer_amd/host/gguf.h"
+#include "../../exactinfer_amd/host/gguf_index.h"
 
 #include <cstdint>
 #include <cstdio>
@@ -104,17 +104,14 @@ int main(int argc, char** argv) {
             out.write(reinterpret_cast<const char*>(b.data()), static_cast<std::streamsize>(b.size()));
         }
         try {
-            ei::GgufFile g(scratch);
+            ei::gguf::Index g(scratch);
             uint64_t sum = 0;
-            for (const ei::GgufTensor& t : g.tensors())
-                for (uint64_t i = 0; i < t.nbytes; ++i) sum += t.data[i];
-            ei::Qwen3Config c = ei::qwen3_config(g);
-            (void)ei::qwen3_tensors(g, c);
+            for (const ei::gguf::TensorSlot& t : g.tensors())
+                for (uint64_t i = 0; i < t.bytes; ++i) sum += t.data[i];
+            (void)ei::gguf::qwen3_config(g);
             ++accepted;
             if (sum == 1) std::printf(" ");  // keeps the reads
-        } catch (const ei::GgufError&) {
-            ++rejected;
-        } catch (const std::runtime_error&) {  // the Qwen3 configuration and shape checks
+        } catch (const ei::gguf::FormatError&) {
             ++rejected;
         } catch (const std::exception& e) {
             std::fprintf(stderr, "iteration %ld: unexpected exception: %s\n", it, e.what());

@@ -1,4 +1,4 @@
-"""The GGUF reader (exactinfer_amd/host/gguf.cpp through include/ei_gguf.h), CPU only.
+"""The GGUF reader (exactinfer_amd/host/gguf_index.cpp and qwen3_schema.cpp through include/ei_gguf.h), CPU only.
 
 Files come from tests/golden/write_tiny_gguf.py (a tiny synthetic Qwen3; no real Qwen3 GGUF
 exists here, so a real file stays unread).  Checked: the tensor table and metadata against the
@@ -324,7 +324,8 @@ def test_mutated_files_under_sanitizers(tmp_path):
     exe = tmp_path / "gguf_fuzz"
     build = subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined",
                             "-fno-sanitize-recover=all", "-fno-omit-frame-pointer", str(here / "cpp" / "gguf_fuzz.cpp"),
-                            str(here.parent / "exactinfer_amd" / "host" / "gguf.cpp"), "-o", str(exe)],
+                            str(here.parent / "exactinfer_amd" / "host" / "gguf_index.cpp"),
+                            str(here.parent / "exactinfer_amd" / "host" / "qwen3_schema.cpp"), "-o", str(exe)],
                            capture_output=True, text=True)
     assert build.returncode == 0, build.stderr
     for i, seed in enumerate(_fuzz_seeds(tmp_path)):
