@@ -119,10 +119,15 @@ class DecodeWorkspace:
     def status(self) -> int:
         """The workspace's sticky status word (uint32 at (nbytes - 256) & ~255; bit 0: the splits of one
         (sequence, KV head) ran on different XCDs, against the placement the in-kernel split
-        merge relies on).  Synchronises the stream."""
-        at = (self.nbytes - 256) & ~255
-        word = self.buf[at:at + 4].cpu()
-        return int(word.view(torch.int32)[0]) & 0xFFFFFFFF
+        merge relies on).  Read through ei_attn_workspace_status, which synchronises the stream."""
+        import ctypes
+        word = ctypes.c_uint32(0)
+        _capi.call("ei_attn_workspace_status", _stream(), self.buf.data_ptr(), self.nbytes, ctypes.byref(word))
+        return int(word.value)
+
+    def check(self) -> None:
+        """Raises EiError (EI_ERR_MERGE) when the status word reports a failed split-merge check."""
+        _capi.call("ei_decode_status_check", self.status())
 
 
 def attn_decode(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos_dev: torch.Tensor, shape: AttnShape,

@@ -84,7 +84,7 @@ int check_rope_fused_decode(int rope_dim, int head_dim) {
 
 EI_API const char* ei_last_error(void) { return g_err.c_str(); }
 
-EI_API int ei_abi_version(void) { return 2; }
+EI_API int ei_abi_version(void) { return 3; }
 
 EI_API int ei_rope_table_fill(float* cs_host, int n_ctx, int rope_dim, double theta) {
     REQUIRE(cs_host != nullptr, "cs_host is null");
@@ -157,6 +157,28 @@ EI_API int ei_attn_workspace_init(ei_stream_t stream, void* ws, size_t ws_bytes)
     return hip_status(ei::launch_ws_clear(static_cast<hipStream_t>(stream), ws, ws_bytes), "workspace clear");
 }
 
+EI_API int ei_attn_workspace_status(ei_stream_t stream, const void* ws, size_t ws_bytes, uint32_t* status) {
+    REQUIRE(ws != nullptr && status != nullptr, "null pointer argument");
+    REQUIRE(ws_bytes >= 256, "workspace of %zu bytes holds no status word", ws_bytes);
+    const char* word = static_cast<const char*>(ws) + ei::ws_status_offset(ws_bytes);
+    uint32_t v = 0;
+    if (int e = hip_status(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "stream sync")) return e;
+    if (int e = hip_status(hipMemcpy(&v, word, sizeof v, hipMemcpyDeviceToHost), "status read")) return e;
+    *status = v;
+    return ok();
+}
+
+EI_API int ei_decode_status_check(uint32_t status) {
+    if (status == 0) return ok();
+    if (status & 1u)
+        return fail(EI_ERR_MERGE,
+                    "decode workspace status 0x%x: the splits of one (sequence, kv head) ran on different XCDs, so "
+                    "the in-kernel split merge may have read stale partials and outputs since the workspace was "
+                    "initialised may be wrong (EI_DECODE_MERGE=launch merges in a second launch)",
+                    status);
+    return fail(EI_ERR_MERGE, "decode workspace status 0x%x: unknown status bits set", status);
+}
+
 namespace {
 
 int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void* ws, size_t ws_bytes, bool fused,
@@ -181,7 +203,7 @@ int decode_common(hipStream_t st, ei::DecodeArgs& a, int n_seq, int max_kv, void
     a.n_xcc = ei::device_xccs();
     REQUIRE(((long)a.units + a.n_xcc) * a.nsplit <= 0x7FFFFFFFL,
             "n_seq %d x n_head_kv %d x %d key splits: more workgroups than one launch takes", n_seq, a.HKV, a.nsplit);
-    a.merge_in_kernel = !launch_combine && ei::decode_merge_in_kernel(p.chunk);
+    a.merge_in_kernel = !launch_combine && ei::decode_merge_in_kernel(p.chunk, a.n_xcc);
     return hip_status(ei::launch_decode(st, a, n_seq, fused), "decode launch");
 }
 

@@ -838,13 +838,16 @@ int device_xccs() {
     return v;
 }
 
-bool decode_merge_in_kernel(int chunk) {
+bool decode_merge_in_kernel(int chunk, int n_xcc) {
     // Chunks of more than 128 keys (the 4-wave streaming kernel) merge in-kernel: configs[3]'s
     // 1024-key chunks run ~4.5% faster than with the second launch.  Short chunks (one tile per
     // wave, e.g. ctx 4096 over 32 splits) keep the second launch: there the partial stores are
     // acknowledged only once the memory queues drain after the stream (0.6-2 us, against
     // 0.18 us on an idle part), which costs more than the launch.  EI_DECODE_MERGE=launch or
-    // =kernel forces either.
+    // =kernel forces either.  The protocol needs the splits of a unit on one XCD (one L2); that
+    // workgroup b runs on XCD b % n_xcc was validated on MI355X in SPX mode (8 XCDs), and with
+    // one XCD there is one L2.  Any other partition merges in the second launch.
+    if (n_xcc != 8 && n_xcc != 1) return false;
     static const int forced = [] {
         const char* e = std::getenv("EI_DECODE_MERGE");
         if (!e) return -1;

@@ -107,7 +107,9 @@ struct DecodeArgs {
 
 hipError_t launch_decode(hipStream_t st, const DecodeArgs& a, int n_seq, bool fused);
 int device_xccs();              // XCDs of the current device
-bool decode_merge_in_kernel(int chunk);  // split merge inside the decode launch for this chunk size
+// split merge inside the decode launch for this chunk size on a device of n_xcc XCDs (only where
+// the placement it relies on was validated: 8 XCDs, or 1)
+bool decode_merge_in_kernel(int chunk, int n_xcc);
 hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes);
 // the decode plan's memory traffic alone, for one sequence of len keys; sink takes one float per workgroup
 hipError_t launch_stream_ceiling(hipStream_t st, const float* kc, const float* vc, int HKV, int len, float* sink);

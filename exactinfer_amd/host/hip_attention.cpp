@@ -60,6 +60,8 @@ void HipAttention::allocate() {
 
     hip_check(hipMalloc(&pos_dev_, sizeof(int)), "position");
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&pos_host_), sizeof(int), hipHostMallocDefault), "pinned position");
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&status_host_), sizeof(uint32_t), hipHostMallocDefault),
+              "pinned status");
     hip_check(hipStreamSynchronize(stream_), "init");
 }
 
@@ -68,12 +70,14 @@ HipAttention::~HipAttention() { release(); }
 void HipAttention::release() noexcept {
     if (stream_) (void)hipStreamSynchronize(stream_);
     if (pos_host_) (void)hipHostFree(pos_host_);
+    if (status_host_) (void)hipHostFree(status_host_);
     if (pos_dev_) (void)hipFree(pos_dev_);
     if (ws_) (void)hipFree(ws_);
     if (pws_) (void)hipFree(pws_);
     if (rope_) (void)hipFree(rope_);
     if (kv_) (void)hipFree(kv_);
     pos_host_ = nullptr;
+    status_host_ = nullptr;
     pos_dev_ = nullptr;
     ws_ = pws_ = nullptr;
     rope_ = kv_ = nullptr;
@@ -83,11 +87,24 @@ void HipAttention::begin_chunk(int pos0, int B) {
     if (B <= 0) throw std::invalid_argument("empty chunk");
     if (B > max_batch_) throw std::invalid_argument("chunk larger than max_batch");
     if (pos0 < 0 || pos0 + B > n_ctx_) throw std::out_of_range("context window full");
-    // the pinned host word is reused: wait until the previous chunk's upload has been consumed
-    hip_check(hipStreamSynchronize(stream_), "chunk sync");
+    // the pinned host word is reused: wait until the previous chunk's upload has been consumed;
+    // the wait also brings the decode workspace's status word, checked here
+    check_status();
     *pos_host_ = pos0;
     hip_check(hipMemcpyAsync(pos_dev_, pos_host_, sizeof(int), hipMemcpyHostToDevice, stream_), "position upload");
     B_ = B;
+}
+
+void HipAttention::raise_on_status(uint32_t status) {
+    if (ei_decode_status_check(status) != EI_OK) throw std::runtime_error(ei_last_error());
+}
+
+void HipAttention::check_status() {
+    // the status word sits where the workspace's size puts it (include/ei_attn.h)
+    const char* word = static_cast<const char*>(ws_) + ((ws_bytes_ - 256) & ~size_t(255));
+    hip_check(hipMemcpyAsync(status_host_, word, sizeof(uint32_t), hipMemcpyDeviceToHost, stream_), "status read");
+    hip_check(hipStreamSynchronize(stream_), "chunk sync");
+    raise_on_status(*status_host_);
 }
 
 float* HipAttention::kcache(int l) const {

@@ -71,6 +71,14 @@ public:
     void project(const float* x, long x_stride, int n_embd, const float* attn_norm, const void* w, int w_type,
                  int n_out, float* qkv, long qkv_stride);
 
+    // Waits for the queued work and throws std::runtime_error if the decode workspace's status
+    // word reports a failed split-merge check (attention outputs may then be wrong).  begin_chunk
+    // does the same check at its own synchronisation, so an engine that starts every chunk or
+    // token with begin_chunk learns of a failure no later than the next token.
+    void check_status();
+    // Throws std::runtime_error for a non-zero status word (ei_decode_status_check's message).
+    static void raise_on_status(uint32_t status);
+
     // Device views of layer l's cache, [n_ctx][n_head_kv][128] fp32.
     float* kcache(int l) const;
     float* vcache(int l) const;
@@ -92,6 +100,7 @@ private:
     size_t pws_bytes_ = 0;
     int* pos_dev_ = nullptr;
     int* pos_host_ = nullptr;  // pinned
+    uint32_t* status_host_ = nullptr;  // pinned copy of the decode workspace's status word
     float scale_;
 };
 

@@ -39,7 +39,9 @@ enum {
     EI_OK = 0,
     EI_ERR_ARG = 1,         /* invalid argument (shape, alignment, null pointer, size) */
     EI_ERR_UNSUPPORTED = 2, /* valid in the reference but not built here (e.g. head_dim != 128) */
-    EI_ERR_HIP = 3          /* a HIP runtime call or kernel launch failed */
+    EI_ERR_HIP = 3,         /* a HIP runtime call or kernel launch failed */
+    EI_ERR_MERGE = 4        /* a decode workspace's status word reports a failed split-merge check:
+                               outputs of the in-kernel merge on it may be wrong */
 };
 
 /* Message of the last failure on this thread ("" if none).  Valid until the next call. */
@@ -120,10 +122,23 @@ int ei_qkv_prepare(ei_stream_t stream, float* qkv, int rows, long row_stride, in
  * leaves the counters at zero again.  Status bit 0 is set, and stays set, if the splits of one
  * (sequence, kv head) were ever found on different XCDs, against the round-robin placement the
  * in-kernel merge relies on (never seen on MI355X; that merge is then unreliable: set
- * EI_DECODE_MERGE=launch for the two-launch combine).  Calls that share a workspace must not
- * overlap in time. */
+ * EI_DECODE_MERGE=launch for the two-launch combine).  The in-kernel merge is only chosen on a
+ * device whose XCD count is one the placement was validated on (8, an MI355X in SPX mode, or 1,
+ * one L2); elsewhere every call merges in the second launch.  Calls that share a workspace must
+ * not overlap in time. */
 size_t ei_attn_decode_ws_bytes(int n_seq, int n_head, int n_head_kv, int max_kv);
 int ei_attn_workspace_init(ei_stream_t stream, void* ws, size_t ws_bytes);
+
+/* Reads a decode workspace's status word into *status once the work queued on `stream` has
+ * finished (a host synchronisation: not for use under graph capture).  No counterpart in the
+ * reference, whose split combine is always a second launch (src/cuda/model_cuda.cu:1097-1111):
+ * it is how a caller learns that the in-kernel merge saw a broken placement. */
+int ei_attn_workspace_status(ei_stream_t stream, const void* ws, size_t ws_bytes, uint32_t* status);
+
+/* Host-only: EI_OK for a status word of 0, else EI_ERR_MERGE with a message naming the failed
+ * check (ei_last_error).  HipAttention and other callers turn a read status word into an error
+ * with it. */
+int ei_decode_status_check(uint32_t status);
 
 /* Single-sequence decode attention: q [n_head][128] (already normed + roped), cache rows
  * 0..*pos_dev visible (T = *pos_dev + 1 <= max_kv), out [n_head][128].

@@ -19,6 +19,7 @@
 // rows and F32 weights, in the same chunks, checked against the CPU path's rmsnorm + matvec
 // (src/model.cpp:176-179) within 1e-5 of the row's rms; the attention checks then run on them.
 // Prints one JSON line; exit status 0 when every check passes.
+// "engine_test status <word>" runs no GPU work: see status_mode.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -52,7 +53,24 @@ static double rel_err_row(const float* got, const float* ref, int n) {
     return e;
 }
 
+// "engine_test status <word>": HipAttention's reaction to a decode workspace status word, with no
+// GPU call (the word stands in for one read back from a workspace).  Prints {"thrown": ..., "what": ...}.
+static int status_mode(const char* word) {
+    const uint32_t w = static_cast<uint32_t>(std::strtoul(word, nullptr, 0));
+    try {
+        ei::HipAttention::raise_on_status(w);
+        std::printf("{\"thrown\": false, \"what\": \"\"}\n");
+    } catch (const std::runtime_error& e) {
+        std::string what = e.what();
+        for (char& c : what)
+            if (c == '"' || c == '\\') c = '\'';
+        std::printf("{\"thrown\": true, \"what\": \"%s\"}\n", what.c_str());
+    }
+    return 0;
+}
+
 int main(int argc, char** argv) {
+    if (argc == 3 && std::string(argv[1]) == "status") return status_mode(argv[2]);
     bool use_graph = false, use_project = false, bad_args = argc < 8;
     for (int i = 8; i < argc; ++i) {
         if (std::string(argv[i]) == "graph") use_graph = true;

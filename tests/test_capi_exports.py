@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     L = _capi.lib()
     for name in _declared():
         assert isinstance(getattr(L, name), ctypes._CFuncPtr), name
-    assert L.ei_abi_version() == 2
+    assert L.ei_abi_version() == 3
 
 
 def test_rope_table_fill_host_matches_oracle(orc):
