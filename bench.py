@@ -58,7 +58,8 @@ def parse():
                     help="skip the parity-case shapes reported beside the headline (configs[3], configs[4] contiguous "
                          "and paged, configs[2] in 512-token chunks)")
     ap.add_argument("--only", choices=["decode", "decode-groups", "prefill", "prefill-chunked", "prefill-groups",
-                                       "longctx", "batched", "batched-paged", "stream-ceiling", "configs0", "project"],
+                                       "longctx", "batched", "batched-paged", "stream-ceiling", "read-ceiling", "configs0",
+                                       "project"],
                     default=None,
                     help="run one workload and print its result (decode: the headline line without prefill and extras; "
                          "decode-groups / prefill-groups: the dense Qwen3 GQA group sizes)")
@@ -190,6 +191,40 @@ def bench_stream_ceiling(torch, A, H, HKV, n_layer, ctx, reps=50, seed=1000):
     kv_bytes = 2.0 * ctx * kd * 4
     return {"kernel_ms": ms, "kv_bytes_per_launch": kv_bytes, "gbs": kv_bytes / (ms * 1e-3) / 1e9,
             "decode_bytes_per_launch": A.decode_bytes(ctx, H, HKV)}
+
+
+def bench_read_ceiling(torch, A, nbytes=2 * 4096 * 8 * D * 4, n_layer=36, reps=50, seed=1000):
+    """The read ceiling of one decode launch's bytes (ei_read_ceiling): n_layer launches, each a plain
+    non-temporal streaming read of its own nbytes buffer (configs[1]'s K+V per layer by default: no
+    launch finds its bytes in a cache), replayed as one graph, for 256, 512 and 1024 workgroups of
+    256 threads (and more where a thread would otherwise take over 64 loads).  Returns each grid's
+    time per launch and the best."""
+    from exactinfer_amd import _capi
+    dev = "cuda"
+    buf = torch.empty((n_layer, nbytes // 4), dtype=torch.float32, device=dev)
+    for l in range(n_layer):
+        A.synth_fill(buf[l], seed + l)
+    sink = torch.empty((4096 * 4,), dtype=torch.float32, device=dev)
+    res = {"bytes_per_launch": nbytes, "launches_per_graph": n_layer}
+    best = None
+    for n_wg in (256, 512, 1024, 2048, 4096):
+        if n_wg > 1024 and nbytes <= 1024 * 256 * 64 * 16:
+            break
+        if nbytes > n_wg * 256 * 64 * 16:
+            continue
+
+        def run():
+            for l in range(n_layer):
+                _capi.call("ei_read_ceiling", A._stream(), buf[l].data_ptr(), nbytes, n_wg, sink.data_ptr())
+
+        ms = graph_ms(torch, run, reps=reps, warm=5) / n_layer
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[f"wg{n_wg}"] = {"kernel_us": round(ms * 1e3, 3), "gbs": round(gbs, 1)}
+        if best is None or gbs > best[1]:
+            best = (n_wg, gbs, ms)
+    res.update({"best_workgroups": best[0], "kernel_us": round(best[2] * 1e3, 3), "gbs": best[1]})
+    del buf
+    return res
 
 
 def bench_project(torch, A, E=2560, H=32, HKV=8, n_layer=36, seed=7000):
@@ -556,8 +591,26 @@ def bench_configs0_gpu(torch, A):
     for i, t in enumerate(range(P, n_ctx)):
         A.decode_step(qkv[t:t + 1], kc, vc, shape, gam[0], gam[1], cs, dws, pos_dev=poss[i])
     dec_ms = tm.stop_ms()
+
+    # the same work as HIP graphs, the way an engine replays its steps: the prompt's prefill step as
+    # one graph, the 128 decode steps (one fused launch + split merge each, own position word) as another
+    def prefill_only():
+        A.prefill_step(qkv[:P], kc, vc, shape, gam[0], gam[1], cs, pos0, pws, B=P)
+
+    def decode_all():
+        for i, t in enumerate(range(P, n_ctx)):
+            A.decode_step(qkv[t:t + 1], kc, vc, shape, gam[0], gam[1], cs, dws, pos_dev=poss[i])
+
+    qkv.copy_(src)
+    pre_g = graph_ms(torch, prefill_only, reps=20, warm=2)
+    dec_g = graph_ms(torch, decode_all, reps=20, warm=2)
+    dec_bytes = sum(A.decode_bytes(t + 1, H, HKV) for t in range(P, n_ctx))
     return {"prefill_ms": pre_ms, "decode_ms_128_steps": dec_ms, "decode_us_per_step": dec_ms * 1e3 / G,
-            "note": "eager launches, one layer: launch-latency bound at this size"}
+            "note": "eager launches, one layer: launch-latency bound at this size",
+            "graph": True, "graph_prefill_ms": pre_g,
+            "graph_prefill_tflops": A.flops_causal(P, 0, H) / (pre_g * 1e-3) / 1e12,
+            "graph_decode_ms_128_steps": dec_g, "graph_decode_us_per_step": dec_g * 1e3 / G,
+            "graph_decode_gbs": dec_bytes / (dec_g * 1e-3) / 1e9}
 
 
 def main():
@@ -632,6 +685,18 @@ def main():
         res["stream_ceiling"]["longctx"] = {"kernel_ms": round(lc["kernel_ms"], 4), "gbs": round(lc["gbs"], 1),
                                             "pct_hbm_peak": round(100 * lc["gbs"] / HBM_PEAK_GBS, 2)}
         log(json.dumps(res["stream_ceiling"]))
+    if args.only in (None, "decode", "read-ceiling"):
+        log("read ceiling of configs[1]'s per-layer bytes ...")
+        res["read_ceiling"] = bench_read_ceiling(torch, A)
+        log(json.dumps(res["read_ceiling"]))
+    if args.only == "read-ceiling":  # the same over the per-launch sizes of the other kernels
+        res["read_ceiling"]["by_size"] = {}
+        for mb in (4, 8.9, 12.9, 16.7, 31.5, 67, 134, 268):
+            nb = int(mb * 1e6) // 4096 * 4096
+            r = bench_read_ceiling(torch, A, nbytes=nb, n_layer=max(4, min(36, int(1.2e9 // nb))), reps=20)
+            res["read_ceiling"]["by_size"][f"{nb / 1e6:.1f}MB"] = {k: r[k] for k in ("best_workgroups", "kernel_us",
+                                                                                     "gbs")}
+            log(f"{nb / 1e6:.1f} MB: " + json.dumps(r))
     if extra or args.only == "project":
         log("QKV projection at Qwen3-4B shape ...")
         res["project"] = bench_project(torch, A)
@@ -644,7 +709,7 @@ def main():
         print(json.dumps(res))
         return
     cpu = None if args.no_cpu else cpu_baseline()
-    dec, pre = res["decode"], res.get("prefill")
+    dec, pre, rc = res["decode"], res.get("prefill"), res["read_ceiling"]
     line = {
         "metric": "attn decode GB/s (% of HBM peak) @4B ctx4096; causal prefill attn TFLOP/s",
         "value": round(dec["gbs"], 2),
@@ -666,7 +731,12 @@ def main():
                      "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": profile_traffic("decode_configs1_hbm_traffic.md"),
                      "kernel": "k_decode<4,true,8> + k_combine<4> (one layer, graph-timed)",
-                     "kernel_us": round(dec["kernel_ms"] * 1e3, 3), "bytes_per_launch": dec["bytes_per_launch"]},
+                     "kernel_us": round(dec["kernel_ms"] * 1e3, 3), "bytes_per_launch": dec["bytes_per_launch"],
+                     # what a plain streaming read of the same K+V bytes per launch reaches (36 launches
+                     # in one graph, best of 256/512/1024 workgroups), and this kernel's fraction of it
+                     "ceiling_gbs": round(rc["gbs"], 1), "ceiling_us": rc["kernel_us"],
+                     "ceiling_frac": round(dec["kernel_gbs"] / rc["gbs"], 4),
+                     "ceiling_pct_hbm_peak": round(100 * rc["gbs"] / HBM_PEAK_GBS, 2)},
         "cpu_baseline": cpu,
     }
     if pre is not None:
@@ -687,7 +757,8 @@ def main():
                                                          "tflops": round(pre["plain_kernel_tflops"], 3)}}}
     # the other configs (parity-test shapes), measured beside the headline for context
     ex = {}
-    for k in ("longctx", "batched", "batched_paged", "prefill_chunked", "stream_ceiling", "configs0", "project"):
+    for k in ("longctx", "batched", "batched_paged", "prefill_chunked", "stream_ceiling", "read_ceiling", "configs0",
+              "project"):
         if k in res:
             ex[k] = {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in res[k].items()}
             if "gbs" in res[k]:

@@ -271,6 +271,14 @@ int ei_prefill_step_paged(ei_stream_t stream, float* qkv, long row_stride, float
  * n_head_kv * 256 floats).  Its duration is the floor of a decode launch of that plan. */
 int ei_stream_ceiling(ei_stream_t stream, const float* kc, const float* vc, int n_head_kv, int kv_len, float* sink);
 
+/* Not part of the reference path: a plain streaming read of `bytes` (a multiple of 16, src
+ * 16-byte aligned) with non-temporal 16-byte global loads by n_workgroups workgroups of 256
+ * threads (1..65535, at most 64 loads per thread: bytes <= n_workgroups * 256 KiB; sink holds
+ * n_workgroups * 16 bytes and is written only by chance).  Its
+ * duration bounds any kernel that reads that many bytes per launch: the read ceiling a decode
+ * launch of the same bytes is measured against. */
+int ei_read_ceiling(ei_stream_t stream, const void* src, size_t bytes, int n_workgroups, void* sink);
+
 /* ------------------------------------------------------------------ synthetic inputs
  * Not part of the reference path: fills n floats with the counter-based N(0,1)
  * generator (element e = stream element offset+e of `seed`), multiplying by spike_mult

@@ -52,7 +52,43 @@ def pytest_terminal_summary(terminalreporter):
     for g, (n, r, p, f) in groups.items():
         tr.write_line(f"  group {g}: {n} cases, max vs reference {r:.3e}, max plain |d|/|ref| {p:.3e}"
                       + (f", {f} by the float64 fallback" if f else ""))
+    _write_evidence_json(EVIDENCE, ATTN_RTOL)
     for case, branch, e_ref, e_gx, e_rx, plain in EVIDENCE:
         if branch != "reference":
             extra = "" if e_gx is None else f"; vs float64 {e_gx:.3e} (reference vs float64 {e_rx:.3e})"
             tr.write_line(f"  {branch:16s} {case}: vs reference {e_ref:.3e}{extra}; plain |d|/|ref| {plain:.3e}")
+
+
+def _write_evidence_json(evidence, bar):
+    """The session's parity evidence as JSON, per group of cases: count, worst error against the
+    reference, worst against float64 and the reference's own distance from float64 (where the
+    float64 check ran), cases passed by the float64 fallback, and the plain |d|/|ref| worst.
+    Written to gpurun_out/parity_evidence.json (or $EI_PARITY_JSON)."""
+    import json
+    import os
+    import re
+    groups = {}
+    for case, branch, e_ref, e_gx, e_rx, plain in evidence:
+        g = groups.setdefault(re.sub(r" (seq|row|call) .*$", "", case),
+                              {"cases": 0, "max_vs_reference": 0.0, "max_vs_float64": None,
+                               "reference_vs_float64": None, "float64_fallback": 0, "failed": 0, "max_plain": 0.0})
+        g["cases"] += 1
+        g["max_vs_reference"] = max(g["max_vs_reference"], e_ref)
+        g["max_plain"] = max(g["max_plain"], plain)
+        if e_gx is not None:
+            g["max_vs_float64"] = max(g["max_vs_float64"] or 0.0, e_gx)
+            g["reference_vs_float64"] = max(g["reference_vs_float64"] or 0.0, e_rx)
+        g["float64_fallback"] += branch == "float64 fallback"
+        g["failed"] += branch == "FAILED"
+    out = {"bar": bar, "cases": len(evidence),
+           "worst_vs_reference": max(e[2] for e in evidence),
+           "worst_vs_float64": max((e[3] for e in evidence if e[3] is not None), default=None),
+           "float64_fallback": sum(e[1] == "float64 fallback" for e in evidence),
+           "failed": sum(e[1] == "FAILED" for e in evidence), "groups": groups}
+    path = os.environ.get("EI_PARITY_JSON") or str(ROOT / "gpurun_out" / "parity_evidence.json")
+    try:
+        os.makedirs(os.path.dirname(path), exist_ok=True)
+        with open(path, "w") as f:
+            json.dump(out, f, indent=1, sort_keys=True)
+    except OSError:
+        pass
