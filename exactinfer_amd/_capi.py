@@ -22,6 +22,7 @@ EXPORTS = (
     "ei_attn_decode_ws_bytes", "ei_attn_workspace_init", "ei_attn_decode", "ei_attn_decode_batched",
     "ei_decode_step", "ei_decode_step_noalloc", "ei_attn_decode_paged", "ei_decode_step_paged", "ei_attn_prefill", "ei_attn_prefill_ws_bytes", "ei_attn_prefill_split", "ei_prefill_step", "ei_prefill_step_paged", "ei_qkv_project", "ei_stream_ceiling", "ei_synth_fill",
     "ei_attn_workspace_status", "ei_decode_status_check", "ei_read_ceiling",
+    "ei_qkv_project_max_rows",
     # include/ei_gguf.h
     "ei_gguf_open", "ei_gguf_close", "ei_gguf_version", "ei_gguf_n_tensors", "ei_gguf_tensor", "ei_gguf_find_tensor",
     "ei_gguf_get_int", "ei_gguf_get_float", "ei_gguf_get_str", "ei_gguf_qwen3_config",
@@ -42,6 +43,7 @@ _SIGS = {
     "ei_attn_workspace_status": ([_vp, _vp, _sz, ctypes.POINTER(ctypes.c_uint32)], _i),
     "ei_decode_status_check": ([ctypes.c_uint32], _i),
     "ei_read_ceiling": ([_vp, _vp, _sz, _i, _vp], _i),
+    "ei_qkv_project_max_rows": ([_i], _i),
     "ei_attn_decode": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _i, _vp, _sz], _i),
     "ei_attn_decode_batched": ([_vp, _vp, _l, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp, _sz], _i),
     "ei_decode_step": ([_vp, _vp, _l, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _i, _f, _f, _i,

@@ -3,6 +3,7 @@
 // entry point returns an EI_* status and records a message for ei_last_error().
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -323,9 +324,23 @@ EI_API int ei_decode_step_noalloc(ei_stream_t stream, const float* qkv, long row
                                   float* vc, const int64_t* kv_offset, const int* kv_len, const int* pos_dev, int n_seq,
                                   int n_head, int n_head_kv, int head_dim, const float* q_gamma, const float* k_gamma,
                                   const float* cs, int rope_dim, float eps, float scale, int max_kv) {
-    return decode_step_impl(stream, qkv, row_stride, out, kc, vc, kv_offset, kv_len, pos_dev, n_seq, n_head,
-                            n_head_kv, head_dim, q_gamma, k_gamma, cs, rope_dim, eps, scale, max_kv, nullptr, 0,
-                            true);
+    // Every call on one GPU shares that GPU's static array.  A call issued while another host
+    // thread is still issuing one on the same GPU is refused; calls issued one after another on
+    // different streams can still overlap on the GPU, which the caller must not do.
+    int dev = 0;
+    if (int e = hip_status(hipGetDevice(&dev), "device query")) return e;
+    REQUIRE(dev >= 0 && dev < 64, "device %d out of range", dev);
+    static std::atomic<int> issuing[64];
+    if (issuing[dev].exchange(1, std::memory_order_acquire))
+        return fail(EI_ERR_ARG,
+                    "another ei_decode_step_noalloc call on device %d is being issued by another thread: calls on "
+                    "one GPU share one scratch array and must not overlap",
+                    dev);
+    const int rc = decode_step_impl(stream, qkv, row_stride, out, kc, vc, kv_offset, kv_len, pos_dev, n_seq, n_head,
+                                    n_head_kv, head_dim, q_gamma, k_gamma, cs, rope_dim, eps, scale, max_kv, nullptr,
+                                    0, true);
+    issuing[dev].store(0, std::memory_order_release);
+    return rc;
 }
 
 namespace {
@@ -554,6 +569,8 @@ EI_API int ei_qkv_project(ei_stream_t stream, const float* x, long x_stride, int
                                              eps, w, w_type, n_out, qkv, qkv_stride),
                       "qkv projection launch");
 }
+
+EI_API int ei_qkv_project_max_rows(int n_embd) { return n_embd > 0 ? ei::qkv_project_max_rows(n_embd) : 0; }
 
 EI_API int ei_stream_ceiling(ei_stream_t stream, const float* kc, const float* vc, int n_head_kv, int kv_len,
                              float* sink) {

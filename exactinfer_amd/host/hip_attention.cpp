@@ -121,8 +121,7 @@ void HipAttention::project(const float* x, long x_stride, int n_embd, const floa
                            int w_type, int n_out, float* qkv, long qkv_stride) {
     if (B_ <= 0) throw std::logic_error("project() before begin_chunk()");
     if (n_embd <= 0) throw std::invalid_argument("n_embd");
-    int per = 24576 / n_embd;  // rows per launch (ei_qkv_project stages them in LDS)
-    if (per > 4) per = 4;
+    const int per = ei_qkv_project_max_rows(n_embd);  // rows per launch (staged in LDS)
     if (per < 1) throw std::invalid_argument("n_embd too large for the projection");
     for (int b = 0; b < B_; b += per) {
         const int rows = B_ - b < per ? B_ - b : per;

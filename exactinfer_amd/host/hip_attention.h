@@ -67,7 +67,7 @@ public:
     //   EI_W_Q8_0, EI_W_Q4_K, EI_W_Q6_K); the fused [Wq | Wk | Wv] with n_out = (H + 2 HKV) * 128,
     //   or one segment of it (qkv then points at the segment's first column);
     //   qkv [B][...] output rows (row stride qkv_stride), left raw for layer().
-    // Runs ei_qkv_project over groups of rows (at most min(4, 24576 / n_embd) per launch).
+    // Runs ei_qkv_project over groups of rows (at most ei_qkv_project_max_rows(n_embd) per launch).
     void project(const float* x, long x_stride, int n_embd, const float* attn_norm, const void* w, int w_type,
                  int n_out, float* qkv, long qkv_stride);
 

@@ -82,6 +82,12 @@ enum { EI_W_F32 = 0, EI_W_F16 = 1, EI_W_Q8_0 = 8, EI_W_Q4_K = 12, EI_W_Q6_K = 14
 int ei_qkv_project(ei_stream_t stream, const float* x, long x_stride, int rows, int n_embd, const float* attn_norm,
                    float eps, const void* w, int w_type, int n_out, float* qkv, long qkv_stride);
 
+/* Rows ei_qkv_project takes per launch at this hidden size: min(4, 24576 / n_embd) (the
+ * activations of all rows are staged in LDS); 0 for n_embd <= 0.  Callers with more rows split
+ * them into launches of at most this many.  No counterpart in the reference, whose GEMV takes
+ * any B (src/cuda/model_cuda.cu:300-320). */
+int ei_qkv_project_max_rows(int n_embd);
+
 /* ------------------------------------------------------------------ QK-norm + RoPE
  * In place on `rows` rows of `buf` (row b at buf + b*row_stride, head h at + h*128):
  * per head, RMSNorm with gamma (sum of squares in double, inv = float(1/sqrt(ss/128+eps)),
@@ -182,7 +188,8 @@ int ei_decode_step(ei_stream_t stream, const float* qkv, long row_stride, float*
  * EI_ERR_ARG.  One sequence at H32/HKV8 takes 0.57 MiB up to max_kv 32768; 64 sequences at
  * H16/HKV8 and max_kv 8192 take 4.8 MiB capped (too much) and 0.56 MiB uncapped; 256 sequences
  * at H32/HKV8 and max_kv 4096 take 4.25 MiB even uncapped (rejected).  Every call on one GPU shares that array:
- * calls that overlap in time on one GPU (two streams, two threads) race and must not be made.
+ * calls that overlap in time on one GPU (two streams, two threads) race and must not be made; a
+ * call made while another thread is still inside one on the same GPU is refused (EI_ERR_ARG).
  * The splits are always merged by the second small launch. */
 int ei_decode_step_noalloc(ei_stream_t stream, const float* qkv, long row_stride, float* out, float* kc, float* vc,
                            const int64_t* kv_offset, const int* kv_len, const int* pos_dev, int n_seq, int n_head,

@@ -163,3 +163,11 @@ def test_fused_decode_rope_dim_multiple_of_4():
     with pytest.raises(_capi.EiError, match="rope_dim 62"):
         _capi.call("ei_decode_step_paged", None, p, 6144, p, p, p, p, 8, 16, p, 1, 32, 8, 128, p, p, p, 62, 1e-6,
                    0.1, 128, p, 1 << 30)
+
+
+def test_projection_rows_per_launch():
+    """ei_qkv_project_max_rows: min(4, 24576 / n_embd), the limit HipAttention::project splits by."""
+    from exactinfer_amd import _capi
+    L = _capi.lib()
+    assert [L.ei_qkv_project_max_rows(e) for e in (1024, 2560, 5120, 6144, 8192, 10240, 24577, 0, -5)] == \
+        [4, 4, 4, 4, 3, 2, 0, 0, 0]

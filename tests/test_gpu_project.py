@@ -50,9 +50,12 @@ def _wf(w, wtype):
     return (w if wtype == W_F32 else w.view(np.float16)).astype(np.float64)
 
 
-@pytest.mark.parametrize("wtype", [W_F32, W_F16])
-@pytest.mark.parametrize("E,H,HKV,rows", [(2560, 32, 8, 1), (2560, 32, 8, 4), (1024, 16, 8, 1), (2048, 16, 8, 3),
-                                         (4096, 32, 8, 2), (5120, 40, 8, 1)])
+@pytest.mark.parametrize("wtype,E,H,HKV,rows",
+                         [(wt, *c) for wt in (W_F32, W_F16)
+                          for c in ((2560, 32, 8, 1), (2560, 32, 8, 4), (1024, 16, 8, 1), (2048, 16, 8, 3),
+                                    (4096, 32, 8, 2), (5120, 40, 8, 1))]
+                         # the F16-only hidden sizes, at the most rows a launch takes there (3 and 2)
+                         + [(W_F16, 8192, 64, 8, 3), (W_F16, 10240, 64, 8, 2)])
 def test_qkv_project_matches_oracle(orc, gpu, wtype, E, H, HKV, rows):
     n_out = (H + 2 * HKV) * D
     x = orc.normal((rows, E), 8500 + E) * np.float32(3.0)
@@ -76,8 +79,8 @@ def _qweights(orc, n_out, E, wtype, seed):
 
 
 @pytest.mark.parametrize("wtype", QTYPES)
-@pytest.mark.parametrize("E,H,HKV,rows", [(2560, 32, 8, 1), (2560, 32, 8, 4), (1024, 16, 8, 2), (4096, 32, 8, 1),
-                                         (5120, 40, 8, 3)])
+@pytest.mark.parametrize("E,H,HKV,rows", [(2560, 32, 8, 1), (2560, 32, 8, 4), (1024, 16, 8, 2), (2048, 16, 8, 4),
+                                         (4096, 32, 8, 1), (5120, 40, 8, 3)])
 def test_qkv_project_quantised_matches_oracle(orc, gpu, wtype, E, H, HKV, rows):
     """Q8_0 / Q4_K / Q6_K weights in their GGUF block layout: every output within 1e-5 of
     sum |w h| of the oracle's matvec (decode with the reference's dequant, then dot_f32), and of

@@ -1,6 +1,6 @@
 """The allocation-free fused decode step (ei_decode_step_noalloc) against ei_decode_step with a
-workspace: two calls in a row through the C ABI, the second with a smaller input, each equal
-bit for bit to the workspace entry point on the same state (both merge their splits with the
+workspace: calls in a row through the C ABI (the second with a smaller input than the first, then GQA
+groups 8 and 1), each equal bit for bit to the workspace entry point on the same state (both merge their splits with the
 second launch for these shapes), cache appends included."""
 import ctypes
 
@@ -38,8 +38,12 @@ def _noalloc(gpu, qkv, kc, vc, shape, qg, kg, cs, max_kv, out, pos_dev=None, kv_
 def test_noalloc_decode_step_matches_workspace_step(orc, gpu):
     import torch
     # call 1: configs[1]'s layer (H32/HKV8, ctx 4096, one sequence); call 2: a smaller ragged batch
+    # then GQA groups 8 and 1 (H64/HKV8, H8/HKV8) through the same shared array, one sequence on the
+    # device position and a ragged batch
     cases = [dict(H=32, HKV=8, lens=[4096], max_kv=4096, seed=7000),
-             dict(H=16, HKV=8, lens=[300, 1, 77], max_kv=512, seed=7100)]
+             dict(H=16, HKV=8, lens=[300, 1, 77], max_kv=512, seed=7100),
+             dict(H=64, HKV=8, lens=[2500], max_kv=3000, seed=7400),
+             dict(H=8, HKV=8, lens=[900, 33], max_kv=1024, seed=7500)]
     for c in cases:
         H, HKV, lens = c["H"], c["HKV"], np.array(c["lens"], np.int32)
         shape = gpu.AttnShape(H, HKV)
