@@ -174,9 +174,18 @@ __device__ __forceinline__ void norm_rope_q8(float* row, const float (&g)[16], c
     }
 }
 
+#ifdef EI_EXP_STAMPS
+__device__ unsigned long long g_pstamps[4096 * 16];
+#define PSTAMP(i) do { if (threadIdx.x == 0) g_pstamps[blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memtime(); } while (0)
+#define PSTAMPV(i, v) do { if (threadIdx.x == 0) g_pstamps[blockIdx.x * 16 + (i)] = (unsigned long long)(v); } while (0)
+#else
+#define PSTAMP(i) do { } while (0)
+#define PSTAMPV(i, v) do { } while (0)
+#endif
+
 // kPaged: key t of the sequence sits in pool row btab[t >> bshift] << bshift | (t & mask), the
 // block size 2^bshift >= 32, so a 32-key tile lies in one block and its rows are consecutive.
-template <bool kNormQ, bool kPaged>
+template <bool kNormQ, bool kPaged, bool kEarlyK = false>
 __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __restrict__ q, long q_stride,
                                                            float* __restrict__ out, const float* __restrict__ kc,
                                                            const float* __restrict__ vc,
@@ -192,6 +201,7 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
     constexpr int DMA_PER_WAVE = 16 / GW;  // V DMA instructions per wave per tile (K: twice as many, 32 lanes each)
     extern __shared__ __align__(16) float smem[];
 
+    PSTAMP(0);
     const int L = blockIdx.x;
     const int kvh = L % HKV;
     const int rest = L / HKV;
@@ -224,8 +234,9 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
     // this key group's K0 K1 and V0 V1: K buffers below the staging area for the plain kernel,
     // which fetches q and the first K tiles together; with the in-kernel q norm (q first,
     // then the tiles) a group's four buffers side by side measured 0.7% faster
-    float* gsm = kNormQ ? smem + grp * kGroupF : smem + grp * 2 * kKTileF;
-    float* gsv = kNormQ ? gsm + 2 * kKTileF : smem + kVBaseF + grp * 2 * kVTileF;
+    constexpr bool kGrouped = kNormQ && !kEarlyK;
+    float* gsm = kGrouped ? smem + grp * kGroupF : smem + grp * 2 * kKTileF;
+    float* gsv = kGrouped ? gsm + 2 * kKTileF : smem + kVBaseF + grp * 2 * kVTileF;
     const float sl2 = scale * 1.44269504088896340736f;
 
     // q of unit u reaches LDS by LDS DMA, once per workgroup: row r = 32*slot + j holds query
@@ -314,6 +325,8 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
     lo1 = __builtin_amdgcn_readfirstlane(lo1);
     r1 = __builtin_amdgcn_readfirstlane(r1);
     const int npass = (r0 > 0) + (r1 > 0);
+    PSTAMPV(12, r0);
+    PSTAMPV(13, r1);
 
     for (int pass = 0; pass < npass; ++pass) {
         const bool first_unit = pass == 0 && r0 > 0;  // this pass runs unit `pair`
@@ -488,6 +501,7 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         // i-1), read K(i+1) and V(i) (both landed by the wait + barrier ending i-1).
         // The score tiles alternate between sa and sb (loop unrolled by two).
         if (pass > 0) __syncthreads();  // every wave has stored its rows from the staging area
+        PSTAMP(1 + 5 * pass);
         stage_q(u);
         load_norm(u);
         floatx16 sa, sb;
@@ -511,6 +525,20 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
             if (n_mine > 0) qk(gsm, sa);
             wait_vmcnt<0>();  // K1 and V0
             __syncthreads();
+        } else if constexpr (kEarlyK) {
+            // the first two K tiles fly with the raw q rows and the norm's operands (K buffers lie
+            // outside the staging area): one round trip before the norm instead of two; the first V
+            // tile, which the staging area overlaps, once q is in registers, landing under the
+            // first score chain
+            if (n_mine > 0) dma_k(0, 0);
+            if (n_mine > 1) dma_k(1, 1);
+            wait_vmcnt<0>();
+            read_q();
+            __syncthreads();  // every wave has its q: the staging area is free for the V tiles
+            if (n_mine > 0) dma_v(0, 0);
+            if (n_mine > 0) qk(gsm, sa);
+            wait_vmcnt<0>();  // V0
+            __syncthreads();
         } else {
             wait_vmcnt<0>();
             read_q();
@@ -527,6 +555,7 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
         // paged: the cache row of the K tile fetched at iteration i + 1 is looked up at iteration
         // i (one scalar load in flight across an MFMA stream), and the V tile fetched at i + 1 is
         // the K tile of i, whose row is known by then; tiles past the range read no table entry
+        PSTAMP(2 + 5 * pass);
         auto tile_row = [&](int i) -> uint32_t {  // cache row of this group's i-th tile, or 0
             const int kt = kt_lo + kKS * i + grp;
             return i < n_mine && (kt + 1) * kKT <= T ? crow(kt * kKT) : 0u;
@@ -562,6 +591,7 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
             if (i + 1 < n_it) iter(i + 1, sb, sa);
         }
 
+        PSTAMP(3 + 5 * pass);
         // ---- merge the key groups through LDS (tile buffers are free after the barrier):
         // group g finalises output blocks db = 2g, 2g+1 and hands the other two to its partner
         float* xw = smem + w * (kXchF * 64) + lane;
@@ -613,7 +643,9 @@ __global__ __launch_bounds__(64 * kSlots * kKS) void k_prefill(const float* __re
                     *reinterpret_cast<float4*>(dst0 + ((size_t)bo * H + ho) * D + 4 * col) = v;
             }
         }
+        PSTAMP(4 + 5 * pass);
     }
+    PSTAMP(11);
 }
 
 // Merge of the ksplit shares of every (query, head): grid ceil(B*H/4), 128 threads; thread
@@ -709,15 +741,16 @@ size_t prefill_ws_bytes(int B, int H, int HKV, int max_kv) {
     return align256((size_t)k * rows * kHeadDim * sizeof(float)) + align256((size_t)k * rows * 2 * sizeof(float));
 }
 
-template <bool kNormQ, bool kPaged>
+template <bool kNormQ, bool kPaged, bool kEarlyK = false>
 static hipError_t launch_prefill_kernel(hipStream_t st, unsigned grid, size_t lds, const float* q, long q_stride,
                                         float* out, const float* kc, const float* vc, const int* pos_dev, int B, int H,
                                         int HKV, float scale, int ksplit, float* part_o, float* part_ml,
                                         const float* q_gamma, const float* cs, float eps, const int* btab,
                                         int bshift, int max_blocks) {
     static std::atomic<bool> opted;
-    if (const hipError_t e = opt_in_lds(opted, (const void*)k_prefill<kNormQ, kPaged>, lds); e != hipSuccess) return e;
-    k_prefill<kNormQ, kPaged><<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
+    if (const hipError_t e = opt_in_lds(opted, (const void*)k_prefill<kNormQ, kPaged, kEarlyK>, lds); e != hipSuccess)
+        return e;
+    k_prefill<kNormQ, kPaged, kEarlyK><<<grid, 64 * kSlots * kKS, lds, st>>>(q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
                                                                     ksplit, part_o, part_ml, q_gamma,
                                                                     reinterpret_cast<const float2*>(cs), eps, btab,
                                                                     bshift, max_blocks);
@@ -743,7 +776,14 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
     const bool nq = q_gamma != nullptr, pg = block_table != nullptr;
     hipError_t e;
     if (nq && pg) return hipErrorInvalidValue;  // not built: a paged step norms q in its prologue
-    if (nq)
+    static const int early = [] {  // tuning aid: EI_PREFILL_EARLYK=0/1 forces the q-norm kernel's fetch order
+        const char* v = std::getenv("EI_PREFILL_EARLYK");
+        return v ? std::atoi(v) : -1;
+    }();
+    if (nq && (early == 1 || (early < 0 && ksplit > 1)))
+        e = launch_prefill_kernel<true, false, true>(st, grid, lds, q, q_stride, out, kc, vc, pos_dev, B, H, HKV,
+                                                     scale, ksplit, part_o, part_ml, q_gamma, cs, eps, nullptr, 0, 0);
+    else if (nq)
         e = launch_prefill_kernel<true, false>(st, grid, lds, q, q_stride, out, kc, vc, pos_dev, B, H, HKV, scale,
                                                ksplit, part_o, part_ml, q_gamma, cs, eps, nullptr, 0, 0);
     else if (pg)
@@ -762,3 +802,9 @@ hipError_t launch_prefill(hipStream_t st, const float* q, long q_stride, float* 
 }
 
 }  // namespace ei
+
+#ifdef EI_EXP_STAMPS
+extern "C" __attribute__((visibility("default"))) int ei_diag_prefill_stamps(void* host, size_t n) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ei::g_pstamps), n * 8, 0, hipMemcpyDeviceToHost);
+}
+#endif
