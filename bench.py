@@ -63,6 +63,8 @@ def parse():
                     default=None,
                     help="run one workload and print its result (decode: the headline line without prefill and extras; "
                          "decode-groups / prefill-groups: the dense Qwen3 GQA group sizes)")
+    ap.add_argument("--read-ceiling-sizes", action="store_true",
+                    help="with --only read-ceiling: also the per-launch sizes of the projection and prefill kernels")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
     return ap.parse_args()
@@ -689,7 +691,7 @@ def main():
         log("read ceiling of configs[1]'s per-layer bytes ...")
         res["read_ceiling"] = bench_read_ceiling(torch, A)
         log(json.dumps(res["read_ceiling"]))
-    if args.only == "read-ceiling":  # the same over the per-launch sizes of the other kernels
+    if args.only == "read-ceiling" and args.read_ceiling_sizes:  # the per-launch sizes of the other kernels
         res["read_ceiling"]["by_size"] = {}
         for mb in (4, 8.9, 12.9, 16.7, 31.5, 67, 134, 268):
             nb = int(mb * 1e6) // 4096 * 4096
