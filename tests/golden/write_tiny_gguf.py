@@ -35,7 +35,8 @@ def _val(t: int, value) -> bytes:
     if t == T_ARRAY:  # value = (element type, list of elements)
         et, items = value
         return struct.pack("<IQ", et, len(items)) + b"".join(_val(et, x) for x in items)
-    fmt = {T_U32: "<I", T_I32: "<i", T_F32: "<f", T_U64: "<Q", T_F64: "<d"}[t]
+    fmt = {0: "<B", 1: "<b", 2: "<H", 3: "<h", T_U32: "<I", T_I32: "<i", T_F32: "<f", 7: "<B", T_U64: "<Q",
+           11: "<q", T_F64: "<d"}[t]
     return struct.pack(fmt, value)
 
 

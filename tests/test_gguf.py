@@ -337,3 +337,56 @@ def test_mutated_files_under_sanitizers(tmp_path):
         assert r.returncode == 0, f"{seed.name}: {r.stderr[-3000:]}"
         ok, accepted, rejected = r.stdout.split()[-3:]
         assert ok == "ok" and int(accepted) > 0 and int(rejected) > 0, r.stdout[-200:]
+
+
+def test_metadata_value_types(tmp_path, model):
+    """Every GGUF scalar type reads back through the typed accessors: integers (signed ones
+    sign-extended, bools as 0/1) through get_int and get_float, reals through get_float only;
+    arrays of every element type are accepted and skipped."""
+    from exactinfer_amd.gguf import GgufError, GgufFile
+    extra = [("t.u8", 0, 250), ("t.i8", 1, -7), ("t.u16", 2, 65000), ("t.i16", 3, -30000), ("t.u32", T_U32, 4000000000),
+             ("t.i32", T_I32, -2000000000), ("t.bool", 7, 1), ("t.u64", 10, (1 << 63) - 1), ("t.i64", 11, -(1 << 62)),
+             ("t.f32", T_F32, 0.25), ("t.f64", 12, -1.5e300), ("t.str", T_STRING, "x" * 300)]
+    arrays = [(f"a.{t}", T_ARRAY, (t, vals)) for t, vals in
+              ((0, [1, 2]), (1, [-1]), (2, [3]), (3, [-4]), (T_U32, [5]), (T_I32, [-6]), (T_F32, [0.5]), (7, [0, 1]),
+               (T_STRING, ["a", "bc", ""]), (10, [7]), (11, [-8]), (12, [1e-300]))]
+    p = _write(tmp_path, model, meta=qwen3_metadata(model) + extra + arrays + [("a.empty", T_ARRAY, (T_U32, []))])
+    with GgufFile(p) as g:
+        for key, t, v in extra:
+            if t in (T_F32, 12):
+                assert g.get_float(key) == v
+                with pytest.raises(GgufError, match="not an integer"):
+                    g.get_int(key)
+            elif t == T_STRING:
+                assert g.get_str(key) == v
+            else:
+                assert g.get_int(key) == v and g.get_float(key) == float(v), key
+        with pytest.raises(GgufError, match="not an integer"):
+            g.get_int("a.0")  # an array is not a scalar
+        assert g.qwen3_config()["n_layer"] == model.n_layer
+
+
+@pytest.mark.parametrize("entry,match", [
+    (("t.bool", 7, 2), "bool value 2"),
+    (("t.u64", 10, 1 << 63), "does not fit an int64"),
+    (("a.bool", T_ARRAY, (7, [0, 1, 3])), "bool value 3"),
+    (("a.u64", T_ARRAY, (10, [1, (1 << 64) - 1])), "does not fit an int64"),
+    (("a.nested", T_ARRAY, (T_ARRAY, [])), "not supported"),
+    (("a.weird", T_ARRAY, (13, [])), "not supported"),
+])
+def test_metadata_value_errors(tmp_path, model, entry, match):
+    """Values no int64 holds, bools other than 0/1 (scalars and array elements) and arrays of arrays
+    or of unknown types are rejected when the file is opened."""
+    _expect_rejected(_write(tmp_path, model, meta=qwen3_metadata(model) + [entry]), match)
+
+
+def test_metadata_type_and_count_errors(tmp_path, model):
+    raw = _write(tmp_path, model, meta=qwen3_metadata(model) + [("z.last", T_U32, 1)]).read_bytes()
+    from tests.golden.write_tiny_gguf import _s
+    i = raw.index(_s("z.last")) + len(_s("z.last"))
+    _expect_rejected(_patched(tmp_path, raw, i, "<I", 13, "ty13.gguf"), "unknown metadata type 13")
+    raw2 = _write(tmp_path, model, name="arr.gguf",
+                  meta=qwen3_metadata(model) + [("z.arr", T_ARRAY, (T_U32, [1, 2]))]).read_bytes()
+    j = raw2.index(_s("z.arr")) + len(_s("z.arr")) + 8  # value type, element type, then the count
+    _expect_rejected(_patched(tmp_path, raw2, j, "<Q", 1 << 27, "cnt.gguf"), "too long")
+    _expect_rejected(_patched(tmp_path, raw2, j, "<Q", 1 << 20, "cnt2.gguf"), "ends early|past the end|not plausible")
