@@ -19,12 +19,13 @@
 // in a wave butterfly; up to kMaxRows activation rows share each weight load.
 //
 // Quantised weights (Q8_0, Q4_K, Q6_K: the block formats the reference computes with,
-// src/quant.h:21-39) stay in their GGUF block layout.  A wave loads its two rows' bytes
-// (16-byte pieces, or 4-byte ones when a row is not a multiple of 16 bytes), parks them in a
-// wave-private LDS area, and each lane then decodes items of 8 consecutive values (one
-// quarter of a Q8_0 block, an eighth of a 32-value Q4_K or Q6_K sub-block) with the
-// reference's operation order (src/quant.cpp:7-60), so every weight is the float the CPU
-// path's convert_row gives, before the same FMA dot as the float kernels.
+// src/quant.h:21-39) stay in their GGUF block layout.  Each lane decodes items of 16
+// consecutive values (half a Q8_0 block, half a 32-value Q4_K sub-block, a 16-value Q6_K group)
+// of one of its wave's two rows, with the reference's values (src/quant.cpp:7-60), so every
+// weight is the float the CPU path's convert_row gives, before the same FMA dot as the float
+// kernels.  Q4_K blocks are whole 16-byte pieces, so each lane loads the two pieces an item needs
+// straight into registers; Q8_0 and Q6_K rows are loaded as coalesced pieces (16-byte, or 4-byte
+// for Q6_K) and parked in a wave-private LDS area first.
 #include <hip/hip_fp16.h>
 
 #include "common.h"
@@ -261,6 +262,31 @@ __device__ __forceinline__ void decode16(const uint8_t* row, int k, float* wv) {
     }
 }
 
+// Q4_K item from registers: hdr = the block's first 16 bytes (d, dmin, 12 scale bytes), q = the
+// item's 16 bytes of nibbles; sub-block sbj, nibble hi4.  Same arithmetic as decode16<12>.
+__device__ __forceinline__ void decode16_q4k_regs(u32x4_t hdr, u32x4_t q, int sbj, int hi4, float* wv) {
+#pragma clang fp contract(off)
+    const float d = f16_bits(hdr.x), dmin = f16_bits(hdr.x >> 16);
+    const uint32_t p0 = hdr.y, p1 = hdr.z, p2 = hdr.w;
+    auto pb = [&](int n) -> int { return (int)(((n < 4 ? p0 : n < 8 ? p1 : p2) >> (8 * (n & 3))) & 0xFFu); };
+    int sc, m;
+    if (sbj < 4) {
+        sc = pb(sbj) & 63;
+        m = pb(sbj + 4) & 63;
+    } else {
+        sc = (pb(sbj + 4) & 15) | ((pb(sbj - 4) >> 6) << 4);
+        m = (pb(sbj + 4) >> 4) | ((pb(sbj) >> 6) << 4);
+    }
+    const float dl = d * (float)sc, ml = dmin * (float)m;
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t nib = opaque((qw[i] >> (4 * hi4)) & 0x0F0F0F0Fu);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) wv[4 * i + b] = __builtin_fmaf(dl, ubyte_f(nib, b), -ml);
+    }
+}
+
 // Quantised rows: T the GGML type (8, 12, 14), NB activation rows (B <= NB), hidden size E
 // (compile time: the activation, gamma and weight loads are all issued before any is used,
 // activations first, so the norm waits for them alone and overlaps the weight stream).  Row
@@ -293,10 +319,27 @@ __global__ __launch_bounds__(64 * kQWaves) void k_qkv_project_q(const float* __r
     for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int i = 0; i < kEl; ++i) xv[b][i] = b < B ? x[(size_t)b * x_stride + tid + i * 64 * kQWaves] : 0.f;
+    // Q4_K blocks (144 bytes) are whole 16-byte pieces: each lane loads the two pieces each of its
+    // items needs (the block's header with d, dmin and the scales; the item's 16 bytes of nibbles) and
+    // decodes from registers, without staging the row through LDS (5.73-5.75 against 6.07-6.08 us at
+    // Qwen3-4B).  Q8_0 (34-byte) and Q6_K (210-byte) blocks are not piece-aligned and stay staged.
+    constexpr bool kDirect = T == 12;
+    u32x4_t dh[kDirect ? E / 512 : 1], dq[kDirect ? E / 512 : 1];
+    if constexpr (kDirect) {
+        const uint8_t* row = w + (size_t)min(r0 + (lane & 1), n_out - 1) * RB;
+#pragma unroll
+        for (int j = 0; j < E / 512; ++j) {
+            const int k = (lane >> 1) + 32 * j, v = (k & 15) * 16;
+            const uint8_t* blk = row + 144 * (k >> 4);
+            dh[j] = *reinterpret_cast<const u32x4_t*>(blk);
+            dq[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(blk + 16 + 32 * (v >> 6) + (v & 31)));
+        }
+    }
     u32x4_t pc[kQRowsPerWave][wide ? kPer : 1];
     uint32_t pd[kQRowsPerWave][wide ? 1 : kPer];
 #pragma unroll
     for (int rr = 0; rr < kQRowsPerWave; ++rr) {
+        if (kDirect) break;
         const uint8_t* row = w + (size_t)min(r0 + rr, n_out - 1) * RB;
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
@@ -334,6 +377,7 @@ __global__ __launch_bounds__(64 * kQWaves) void k_qkv_project_q(const float* __r
     uint8_t* qrow = reinterpret_cast<uint8_t*>(hs + B * E) + (size_t)wv * kQRowsPerWave * RB;
 #pragma unroll
     for (int rr = 0; rr < kQRowsPerWave; ++rr) {
+        if (kDirect) break;
         uint8_t* dst = qrow + rr * RB;
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
@@ -357,7 +401,12 @@ __global__ __launch_bounds__(64 * kQWaves) void k_qkv_project_q(const float* __r
     for (int j = 0; j < E / 512; ++j) {
         const int k = (lane >> 1) + 32 * j;
         float wf[16];
-        decode16<T>(myrow, k, wf);
+        if constexpr (kDirect) {
+            const int v = (k & 15) * 16;
+            decode16_q4k_regs(dh[j], dq[j], 2 * (v >> 6) + ((v >> 5) & 1), (v >> 5) & 1, wf);
+        } else {
+            decode16<T>(myrow, k, wf);
+        }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             if (b >= B) break;
