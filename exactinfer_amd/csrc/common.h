@@ -276,8 +276,19 @@ __device__ __forceinline__ void norm_rope_head(const float* __restrict__ src, co
 }
 
 // ------------------------------------------------------------------ synthetic inputs
-// Counter-based N(0,1) (Irwin-Hall of twelve 16-bit uniforms from three splitmix64
-// outputs); integer arithmetic and an exact final conversion, identical on every platform.
+// Counter-based N(0,1): element e of stream `seed` is one Box-Muller normal
+// z = sqrt(-2 ln u1) cos(2 pi u2) from two 53-bit uniforms (two splitmix64 outputs), every step an
+// IEEE double addition, subtraction or multiplication in a fixed order (no division, no library
+// call, no contraction), so the GPU fill and the CPU checker produce identical bits.
+//   ln u1:  u1 = m 2^k, m in [sqrt(1/2), sqrt(2)) from the bits; ln m = 2 atanh t,
+//           t = (m - 1) / (m + 1), as t (1 + t^2/3 + ... + t^24/25) (|t| <= 0.172); the
+//           reciprocal by six Newton steps from 7/16 (m + 1 lies in [1.7, 2.5]);
+//   sqrt y: y (1/sqrt y), six Newton steps x (3/2 - y x^2 / 2) from the integer estimate
+//           0x5FE6EB50C7B537A9 - bits(y)/2 (Lomont's constant for doubles);
+//   cos:    quarter turn q = floor(4 u2), f = 4 u2 - q (both exact); the angle f pi/2, or
+//           (1 - f) pi/2 with sine and cosine swapped, lies in [0, pi/4], where Taylor series
+//           to degree 17/18 are exact below 2^-60.
+// Rounded to float once; |z| <= 8.6 (u1 >= 2^-53).
 __host__ __device__ __forceinline__ uint64_t synth_mix64(uint64_t z) {
     z += 0x9E3779B97F4A7C15ull;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -286,16 +297,75 @@ __host__ __device__ __forceinline__ uint64_t synth_mix64(uint64_t z) {
 }
 
 __host__ __device__ __forceinline__ float synth_normal(uint64_t seed, uint64_t e) {
-    const uint64_t base = seed * 0xD1B54A32D192ED03ull + 3ull * e;
-    int64_t s = 0;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const uint64_t h = synth_mix64(base + (uint64_t)k);
-        s += (int64_t)(h & 0xFFFF) + (int64_t)((h >> 16) & 0xFFFF) + (int64_t)((h >> 32) & 0xFFFF) +
-             (int64_t)(h >> 48);
+#pragma clang fp contract(off)
+    const uint64_t base = seed * 0xD1B54A32D192ED03ull + 2ull * e;
+    const uint64_t h1 = synth_mix64(base), h2 = synth_mix64(base + 1ull);
+    const double u1 = (double)((h1 >> 11) + 1ull) * 0x1.0p-53;  // (0, 1]
+    const double u2 = (double)(h2 >> 11) * 0x1.0p-53;           // [0, 1)
+    // ln u1
+    const uint64_t ub = (uint64_t)__builtin_bit_cast(unsigned long long, u1);
+    int k = (int)((ub >> 52) & 0x7FF) - 1023;
+    double m = __builtin_bit_cast(double, (unsigned long long)((ub & 0x000FFFFFFFFFFFFFull) | 0x3FF0000000000000ull));
+    if (m > 1.4142135623730951) {
+        m = m * 0.5;
+        k = k + 1;
     }
-    const int64_t n = s + 6 - 6 * 65536;
-    return (float)n * (1.0f / 65536.0f);
+    const double den = m + 1.0;
+    double r = 0.4375;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) r = r * (2.0 - den * r);
+    constexpr double inv_odd[13] = {1.0,        1.0 / 3.0,  1.0 / 5.0,  1.0 / 7.0,  1.0 / 9.0,
+                                    1.0 / 11.0, 1.0 / 13.0, 1.0 / 15.0, 1.0 / 17.0, 1.0 / 19.0,
+                                    1.0 / 21.0, 1.0 / 23.0, 1.0 / 25.0};
+    const double t = (m - 1.0) * r, t2 = t * t;
+    double poly = inv_odd[12];
+#pragma unroll
+    for (int j = 11; j >= 0; --j) poly = poly * t2 + inv_odd[j];
+    const double ln_u1 = (double)k * 0.6931471805599453 + 2.0 * t * poly;
+    // sqrt(-2 ln u1)
+    const double y = -2.0 * ln_u1;
+    double rad = 0.0;
+    if (y > 0.0) {
+        const unsigned long long yb = __builtin_bit_cast(unsigned long long, y);
+        double x = __builtin_bit_cast(double, 0x5FE6EB50C7B537A9ull - (yb >> 1));
+#pragma unroll
+        for (int i = 0; i < 6; ++i) x = x * (1.5 - 0.5 * y * x * x);
+        rad = y * x;
+    }
+    // cos(2 pi u2)
+    const double v = 4.0 * u2;
+    const int q = (int)v;
+    const double f = v - (double)q;
+    const bool swap = f > 0.5;
+    const double phi = (swap ? 1.0 - f : f) * 1.5707963267948966, p2 = phi * phi;
+    constexpr double inv_fact[19] = {1.0,
+                                     1.0,
+                                     1.0 / 2.0,
+                                     1.0 / 6.0,
+                                     1.0 / 24.0,
+                                     1.0 / 120.0,
+                                     1.0 / 720.0,
+                                     1.0 / 5040.0,
+                                     1.0 / 40320.0,
+                                     1.0 / 362880.0,
+                                     1.0 / 3628800.0,
+                                     1.0 / 39916800.0,
+                                     1.0 / 479001600.0,
+                                     1.0 / 6227020800.0,
+                                     1.0 / 87178291200.0,
+                                     1.0 / 1307674368000.0,
+                                     1.0 / 20922789888000.0,
+                                     1.0 / 355687428096000.0,
+                                     1.0 / 6402373705728000.0};
+    double sn = inv_fact[17], cs = inv_fact[18];
+#pragma unroll
+    for (int j = 15; j >= 1; j -= 2) sn = -sn * p2 + inv_fact[j];  // sin(phi) / phi
+#pragma unroll
+    for (int j = 16; j >= 0; j -= 2) cs = -cs * p2 + inv_fact[j];
+    sn = sn * phi;
+    const double c0 = swap ? sn : cs, s0 = swap ? cs : sn;
+    const double cosv = q == 0 ? c0 : q == 1 ? -s0 : q == 2 ? -c0 : s0;
+    return (float)(rad * cosv);
 }
 
 }  // namespace ei

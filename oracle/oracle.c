@@ -36,8 +36,10 @@
  *   orc_dequant_q4_K,    (src/quant.cpp:7-60) compiled from source (oracle/_ref), on random
  *   orc_dequant_q6_K     blocks; committed golden vectors; closed forms (unit scales give
  *                        the stored integers back).
- *   orc_fill_normal      synthetic-input generator (not a reference function): exact
- *                        integer arithmetic, checked for moments and against the GPU fill.
+ *   orc_fill_normal      synthetic-input generator (not a reference function): Box-Muller
+ *                        from basic double operations, equal bit for bit to float32 of
+ *                        numpy's float64 sqrt/log/cos formula, KS-tested, and equal to the
+ *                        GPU fill.
  */
 #include <math.h>
 #include <stddef.h>
@@ -52,10 +54,21 @@
 #define ORC_API __attribute__((visibility("default")))
 
 /* ------------------------------------------------------------------ synthetic inputs
- * Counter-based generator shared with the GPU fill kernel: element e of stream `seed`
- * is an Irwin-Hall(12) approximation of N(0,1) built from three splitmix64 outputs
- * (twelve 16-bit uniforms).  All arithmetic is integer; the final int->float conversion
- * and the multiply by 2^-16 are exact, so every platform produces identical bits. */
+ * Counter-based generator shared with the GPU fill kernel (exactinfer_amd/csrc/common.h,
+ * synth_normal, the same steps): element e of stream `seed` is one Box-Muller normal,
+ * z = sqrt(-2 ln u1) cos(2 pi u2), from two 53-bit uniforms (two splitmix64 outputs).  Every
+ * step is an IEEE double addition, subtraction or multiplication in a fixed order (no division,
+ * no library call, no contraction), so every platform produces identical bits:
+ *   ln u1    u1 = m 2^k with m in [sqrt(1/2), sqrt(2)) (exact, from the bits);
+ *            ln m = 2 atanh t, t = (m - 1) / (m + 1), as t (1 + t^2/3 + ... + t^24/25)
+ *            (|t| <= 0.172: truncation below 2^-60); the reciprocal by six Newton steps
+ *            from 7/16 (m + 1 lies in [1.7, 2.5]);
+ *   sqrt y   y (1/sqrt y), 1/sqrt y by six Newton steps x (3/2 - y x^2 / 2) from the
+ *            integer estimate 0x5FE6EB50C7B537A9 - bits(y)/2 (Lomont's constant for doubles);
+ *   cos      the quarter turn q = floor(4 u2) and f = 4 u2 - q (both exact); the angle
+ *            f pi/2, or (1 - f) pi/2 with sine and cosine swapped, lies in [0, pi/4], where
+ *            Taylor series to degree 17/18 are exact below 2^-60.
+ * The result is rounded to float once.  |z| <= 8.6 (u1 >= 2^-53). */
 static inline uint64_t orc_mix64(uint64_t z) {
     z += 0x9E3779B97F4A7C15ull;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -63,21 +76,73 @@ static inline uint64_t orc_mix64(uint64_t z) {
     return z ^ (z >> 31);
 }
 
+static inline double orc_bits_double(uint64_t u) {
+    double d;
+    memcpy(&d, &u, 8);
+    return d;
+}
+
+static inline uint64_t orc_double_bits(double d) {
+    uint64_t u;
+    memcpy(&u, &d, 8);
+    return u;
+}
+
 static inline float orc_normal_at(uint64_t seed, uint64_t e) {
-    const uint64_t base = seed * 0xD1B54A32D192ED03ull + 3ull * e;
-    int64_t s = 0;
-    for (int k = 0; k < 3; ++k) {
-        const uint64_t h = orc_mix64(base + (uint64_t)k);
-        s += (int64_t)(h & 0xFFFF) + (int64_t)((h >> 16) & 0xFFFF) + (int64_t)((h >> 32) & 0xFFFF) +
-             (int64_t)(h >> 48);
+    const uint64_t base = seed * 0xD1B54A32D192ED03ull + 2ull * e;
+    const uint64_t h1 = orc_mix64(base), h2 = orc_mix64(base + 1ull);
+    const double u1 = (double)((h1 >> 11) + 1ull) * 0x1.0p-53; /* (0, 1] */
+    const double u2 = (double)(h2 >> 11) * 0x1.0p-53;          /* [0, 1) */
+    /* ln u1 */
+    const uint64_t ub = orc_double_bits(u1);
+    int k = (int)((ub >> 52) & 0x7FF) - 1023;
+    double m = orc_bits_double((ub & 0x000FFFFFFFFFFFFFull) | 0x3FF0000000000000ull); /* [1, 2) */
+    if (m > 1.4142135623730951) {
+        m = m * 0.5;
+        k = k + 1;
     }
-    /* sum of 12 uniforms (h+0.5)/65536 minus 6, scaled by 65536: fits in 21 bits */
-    const int64_t n = s + 6 - 6 * 65536;
-    return (float)n * (1.0f / 65536.0f);
+    const double den = m + 1.0;
+    double r = 0.4375;
+    for (int i = 0; i < 6; ++i) r = r * (2.0 - den * r);
+    static const double inv_odd[13] = {1.0,        1.0 / 3.0,  1.0 / 5.0,  1.0 / 7.0,  1.0 / 9.0,
+                                       1.0 / 11.0, 1.0 / 13.0, 1.0 / 15.0, 1.0 / 17.0, 1.0 / 19.0,
+                                       1.0 / 21.0, 1.0 / 23.0, 1.0 / 25.0};
+    const double t = (m - 1.0) * r, t2 = t * t;
+    double poly = inv_odd[12];
+    for (int j = 11; j >= 0; --j) poly = poly * t2 + inv_odd[j];
+    const double ln_u1 = (double)k * 0.6931471805599453 + 2.0 * t * poly;
+    /* sqrt(-2 ln u1) */
+    const double y = -2.0 * ln_u1;
+    double rad = 0.0;
+    if (y > 0.0) {
+        double x = orc_bits_double(0x5FE6EB50C7B537A9ull - (orc_double_bits(y) >> 1));
+        for (int i = 0; i < 6; ++i) x = x * (1.5 - 0.5 * y * x * x);
+        rad = y * x;
+    }
+    /* cos(2 pi u2) */
+    const double v = 4.0 * u2;
+    const int q = (int)v;
+    const double f = v - (double)q;
+    const int swap = f > 0.5;
+    const double phi = (swap ? 1.0 - f : f) * 1.5707963267948966, p2 = phi * phi;
+    static const double inv_fact[19] = {1.0, 1.0, 1.0 / 2.0, 1.0 / 6.0, 1.0 / 24.0, 1.0 / 120.0, 1.0 / 720.0,
+                                        1.0 / 5040.0, 1.0 / 40320.0, 1.0 / 362880.0, 1.0 / 3628800.0,
+                                        1.0 / 39916800.0, 1.0 / 479001600.0, 1.0 / 6227020800.0,
+                                        1.0 / 87178291200.0, 1.0 / 1307674368000.0, 1.0 / 20922789888000.0,
+                                        1.0 / 355687428096000.0, 1.0 / 6402373705728000.0};
+    double sn = inv_fact[17], cs = inv_fact[18];
+    for (int j = 15; j >= 1; j -= 2) sn = -sn * p2 + inv_fact[j]; /* sin/phi: 1 - p2/3! + ... */
+    for (int j = 16; j >= 0; j -= 2) cs = -cs * p2 + inv_fact[j];
+    sn = sn * phi;
+    const double c0 = swap ? sn : cs, s0 = swap ? cs : sn;
+    const double cosv = q == 0 ? c0 : q == 1 ? -s0 : q == 2 ? -c0 : s0;
+    return (float)(rad * cosv);
 }
 
 ORC_API void orc_fill_normal(float* out, size_t n, uint64_t seed, uint64_t offset) {
-    for (size_t i = 0; i < n; ++i) out[i] = orc_normal_at(seed, offset + i);
+    /* elements are independent (counter-based), so threads change no bit */
+#pragma omp parallel for schedule(static) if (n >= 65536)
+    for (long i = 0; i < (long)n; ++i) out[i] = orc_normal_at(seed, offset + (uint64_t)i);
 }
 
 /* gamma ~ 1 + 0.1 * N(0,1), rounded step by step in float */
