@@ -198,8 +198,9 @@ def bench_stream_ceiling(torch, A, H, HKV, n_layer, ctx, reps=50, seed=1000):
 def bench_read_ceiling(torch, A, nbytes=2 * 4096 * 8 * D * 4, n_layer=36, reps=50, seed=1000):
     """The read ceiling of one decode launch's bytes (ei_read_ceiling): n_layer launches, each a plain
     non-temporal streaming read of its own nbytes buffer (configs[1]'s K+V per layer by default: no
-    launch finds its bytes in a cache), replayed as one graph, for 256, 512 and 1024 workgroups of
-    256 threads (and more where a thread would otherwise take over 64 loads).  Returns each grid's
+    launch finds its bytes in a cache), replayed as one graph, for 128 (up to 64 loads per thread),
+    256, 512 and 1024 workgroups of 256 threads (up to 32 loads per thread, and 2048 or 4096
+    workgroups where 1024 would need more).  Returns each grid's
     time per launch and the best."""
     from exactinfer_amd import _capi
     dev = "cuda"
@@ -209,10 +210,11 @@ def bench_read_ceiling(torch, A, nbytes=2 * 4096 * 8 * D * 4, n_layer=36, reps=5
     sink = torch.empty((4096 * 4,), dtype=torch.float32, device=dev)
     res = {"bytes_per_launch": nbytes, "launches_per_graph": n_layer}
     best = None
-    for n_wg in (256, 512, 1024, 2048, 4096):
-        if n_wg > 1024 and nbytes <= 1024 * 256 * 64 * 16:
+    for n_wg in (128, 256, 512, 1024, 2048, 4096):
+        per_thread = -(-nbytes // (n_wg * 256 * 16))  # 16-byte loads per thread, all in flight
+        if n_wg > 1024 and nbytes <= 1024 * 256 * 32 * 16:
             break
-        if nbytes > n_wg * 256 * 64 * 16:
+        if per_thread > 32 and not (n_wg == 128 and per_thread <= 64):
             continue
 
         def run():

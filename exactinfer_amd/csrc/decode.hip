@@ -925,6 +925,7 @@ __global__ __launch_bounds__(256) void k_read_ceiling(const u32x4* src, size_t n
     u32x4 v[L];
 #pragma unroll
     for (int k = 0; k < L; ++k) v[k] = __builtin_nontemporal_load(src + min(i + k * nthr, n16 - 1));
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first use
     u32x4 acc = v[0];
 #pragma unroll
     for (int k = 1; k < L; ++k) acc ^= v[k];
