@@ -198,10 +198,10 @@ def bench_stream_ceiling(torch, A, H, HKV, n_layer, ctx, reps=50, seed=1000):
 def bench_read_ceiling(torch, A, nbytes=2 * 4096 * 8 * D * 4, n_layer=36, reps=50, seed=1000):
     """The read ceiling of one decode launch's bytes (ei_read_ceiling): n_layer launches, each a plain
     non-temporal streaming read of its own nbytes buffer (configs[1]'s K+V per layer by default: no
-    launch finds its bytes in a cache), replayed as one graph, for 128 (up to 64 loads per thread),
-    256, 512 and 1024 workgroups of 256 threads (up to 32 loads per thread, and 2048 or 4096
-    workgroups where 1024 would need more).  Returns each grid's
-    time per launch and the best."""
+    launch finds its bytes in a cache), replayed as one graph, for 128, 256, 512 and 1024 workgroups
+    of 256 threads (2048 or 4096 where 1024 would need over 64 loads per thread), each with the loads
+    interleaved with their uses by the compiler and with every load issued first.  Returns each
+    variant's time per launch and the best."""
     from exactinfer_amd import _capi
     dev = "cuda"
     buf = torch.empty((n_layer, nbytes // 4), dtype=torch.float32, device=dev)
@@ -211,22 +211,27 @@ def bench_read_ceiling(torch, A, nbytes=2 * 4096 * 8 * D * 4, n_layer=36, reps=5
     res = {"bytes_per_launch": nbytes, "launches_per_graph": n_layer}
     best = None
     for n_wg in (128, 256, 512, 1024, 2048, 4096):
-        per_thread = -(-nbytes // (n_wg * 256 * 16))  # 16-byte loads per thread, all in flight
-        if n_wg > 1024 and nbytes <= 1024 * 256 * 32 * 16:
+        per_thread = -(-nbytes // (n_wg * 256 * 16))  # 16-byte loads per thread
+        if n_wg > 1024 and nbytes <= 1024 * 256 * 64 * 16:
             break
-        if per_thread > 32 and not (n_wg == 128 and per_thread <= 64):
+        if per_thread > 64:
             continue
+        for all_in_flight in (0, 1):  # loads interleaved with their uses by the compiler, or all issued first
+            if all_in_flight and per_thread > 32 and n_wg != 128:
+                continue
 
-        def run():
-            for l in range(n_layer):
-                _capi.call("ei_read_ceiling", A._stream(), buf[l].data_ptr(), nbytes, n_wg, sink.data_ptr())
+            def run():
+                for l in range(n_layer):
+                    _capi.call("ei_read_ceiling", A._stream(), buf[l].data_ptr(), nbytes, n_wg, all_in_flight,
+                               sink.data_ptr())
 
-        ms = graph_ms(torch, run, reps=reps, warm=5) / n_layer
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        res[f"wg{n_wg}"] = {"kernel_us": round(ms * 1e3, 3), "gbs": round(gbs, 1)}
-        if best is None or gbs > best[1]:
-            best = (n_wg, gbs, ms)
-    res.update({"best_workgroups": best[0], "kernel_us": round(best[2] * 1e3, 3), "gbs": best[1]})
+            ms = graph_ms(torch, run, reps=reps, warm=5) / n_layer
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            res[f"wg{n_wg}" + ("_all" if all_in_flight else "")] = {"kernel_us": round(ms * 1e3, 3),
+                                                                   "gbs": round(gbs, 1)}
+            if best is None or gbs > best[1]:
+                best = (f"{n_wg}" + (" all loads in flight" if all_in_flight else ""), gbs, ms)
+    res.update({"best_grid": best[0], "kernel_us": round(best[2] * 1e3, 3), "gbs": best[1]})
     del buf
     return res
 
@@ -698,7 +703,7 @@ def main():
         for mb in (4, 8.9, 12.9, 16.7, 31.5, 67, 134, 268):
             nb = int(mb * 1e6) // 4096 * 4096
             r = bench_read_ceiling(torch, A, nbytes=nb, n_layer=max(4, min(36, int(1.2e9 // nb))), reps=20)
-            res["read_ceiling"]["by_size"][f"{nb / 1e6:.1f}MB"] = {k: r[k] for k in ("best_workgroups", "kernel_us",
+            res["read_ceiling"]["by_size"][f"{nb / 1e6:.1f}MB"] = {k: r[k] for k in ("best_grid", "kernel_us",
                                                                                      "gbs")}
             log(f"{nb / 1e6:.1f} MB: " + json.dumps(r))
     if extra or args.only == "project":

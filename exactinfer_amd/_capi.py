@@ -42,7 +42,7 @@ _SIGS = {
     "ei_attn_workspace_init": ([_vp, _vp, _sz], _i),
     "ei_attn_workspace_status": ([_vp, _vp, _sz, ctypes.POINTER(ctypes.c_uint32)], _i),
     "ei_decode_status_check": ([ctypes.c_uint32], _i),
-    "ei_read_ceiling": ([_vp, _vp, _sz, _i, _vp], _i),
+    "ei_read_ceiling": ([_vp, _vp, _sz, _i, _i, _vp], _i),
     "ei_qkv_project_max_rows": ([_i], _i),
     "ei_attn_decode": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _i, _vp, _sz], _i),
     "ei_attn_decode_batched": ([_vp, _vp, _l, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp, _sz], _i),

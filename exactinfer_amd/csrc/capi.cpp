@@ -581,13 +581,15 @@ EI_API int ei_stream_ceiling(ei_stream_t stream, const float* kc, const float* v
                       "stream ceiling launch");
 }
 
-EI_API int ei_read_ceiling(ei_stream_t stream, const void* src, size_t bytes, int n_workgroups, void* sink) {
+EI_API int ei_read_ceiling(ei_stream_t stream, const void* src, size_t bytes, int n_workgroups, int all_in_flight,
+                           void* sink) {
     REQUIRE(src && sink, "null pointer argument");
     REQUIRE(aligned16(src) && aligned16(sink), "pointers must be 16-byte aligned");
     REQUIRE(bytes % 16 == 0 && bytes > 0, "bytes %zu must be a positive multiple of 16", bytes);
     REQUIRE(n_workgroups > 0 && n_workgroups <= 65535, "n_workgroups %d out of range", n_workgroups);
     REQUIRE(bytes <= (size_t)n_workgroups * 256 * 64 * 16, "bytes %zu: more than 64 loads per thread", bytes);
-    return hip_status(ei::launch_read_ceiling(static_cast<hipStream_t>(stream), src, bytes, n_workgroups, sink),
+    return hip_status(ei::launch_read_ceiling(static_cast<hipStream_t>(stream), src, bytes, n_workgroups,
+                                              all_in_flight != 0, sink),
                       "read ceiling launch");
 }
 

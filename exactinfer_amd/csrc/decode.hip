@@ -913,38 +913,46 @@ hipError_t launch_stream_ceiling(hipStream_t st, const float* kc, const float* v
 }
 
 // A plain streaming read: `bytes` (a multiple of 16) read once with non-temporal 16-byte global
-// loads, consecutive lanes on consecutive 16-byte pieces, all L loads of a thread issued before
-// any is consumed (L the smallest of 1, 2, 4, ..., 64 that covers the buffer with this grid;
-// indices past the end are clamped to the last piece, so every load is unconditional).  No LDS
-// and no arithmetic beyond an XOR that keeps the loads; a workgroup writes to sink only if that
-// XOR hits one fixed value.  Its duration is what any kernel reading this many bytes per launch
-// with this many workgroups can reach on this part.
-template <int L>
+// loads, consecutive lanes on consecutive 16-byte pieces, L loads per thread (L the smallest of
+// 1, 2, 4, ..., 64 that covers the buffer with this grid; indices past the end are clamped to the
+// last piece, so every load is unconditional).  kAll: every load of a thread is issued before any
+// is used (a scheduling barrier; L x 4 registers); otherwise the compiler interleaves loads and
+// uses, keeping fewer registers and more waves.  No LDS and no arithmetic beyond an XOR that keeps
+// the loads; a workgroup writes to sink only if that XOR hits one fixed value.  Its duration is
+// what a kernel reading this many bytes per launch with this grid can reach on this part.
+template <int L, bool kAll>
 __global__ __launch_bounds__(256) void k_read_ceiling(const u32x4* src, size_t n16, u32x4* sink) {
     const size_t nthr = (size_t)gridDim.x * 256, i = (size_t)blockIdx.x * 256 + threadIdx.x;
     u32x4 v[L];
 #pragma unroll
     for (int k = 0; k < L; ++k) v[k] = __builtin_nontemporal_load(src + min(i + k * nthr, n16 - 1));
-    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first use
+    if constexpr (kAll) __builtin_amdgcn_sched_barrier(0);
     u32x4 acc = v[0];
 #pragma unroll
     for (int k = 1; k < L; ++k) acc ^= v[k];
     if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9e3779b9u) sink[blockIdx.x] = acc;
 }
 
-hipError_t launch_read_ceiling(hipStream_t st, const void* src, size_t bytes, int n_wg, void* sink) {
+template <bool kAll>
+static hipError_t launch_read_ceiling_t(hipStream_t st, const u32x4* s, size_t n16, size_t per, int n_wg, u32x4* o) {
+    if (per <= 1) k_read_ceiling<1, kAll><<<n_wg, 256, 0, st>>>(s, n16, o);
+    else if (per <= 2) k_read_ceiling<2, kAll><<<n_wg, 256, 0, st>>>(s, n16, o);
+    else if (per <= 4) k_read_ceiling<4, kAll><<<n_wg, 256, 0, st>>>(s, n16, o);
+    else if (per <= 8) k_read_ceiling<8, kAll><<<n_wg, 256, 0, st>>>(s, n16, o);
+    else if (per <= 16) k_read_ceiling<16, kAll><<<n_wg, 256, 0, st>>>(s, n16, o);
+    else if (per <= 32) k_read_ceiling<32, kAll><<<n_wg, 256, 0, st>>>(s, n16, o);
+    else if (per <= 64) k_read_ceiling<64, kAll><<<n_wg, 256, 0, st>>>(s, n16, o);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_read_ceiling(hipStream_t st, const void* src, size_t bytes, int n_wg, bool all_in_flight,
+                               void* sink) {
     const size_t n16 = bytes / 16, nthr = (size_t)n_wg * 256, per = (n16 + nthr - 1) / nthr;
     const u32x4* s = static_cast<const u32x4*>(src);
     u32x4* o = static_cast<u32x4*>(sink);
-    if (per <= 1) k_read_ceiling<1><<<n_wg, 256, 0, st>>>(s, n16, o);
-    else if (per <= 2) k_read_ceiling<2><<<n_wg, 256, 0, st>>>(s, n16, o);
-    else if (per <= 4) k_read_ceiling<4><<<n_wg, 256, 0, st>>>(s, n16, o);
-    else if (per <= 8) k_read_ceiling<8><<<n_wg, 256, 0, st>>>(s, n16, o);
-    else if (per <= 16) k_read_ceiling<16><<<n_wg, 256, 0, st>>>(s, n16, o);
-    else if (per <= 32) k_read_ceiling<32><<<n_wg, 256, 0, st>>>(s, n16, o);
-    else if (per <= 64) k_read_ceiling<64><<<n_wg, 256, 0, st>>>(s, n16, o);
-    else return hipErrorInvalidValue;
-    return hipGetLastError();
+    return all_in_flight ? launch_read_ceiling_t<true>(st, s, n16, per, n_wg, o)
+                         : launch_read_ceiling_t<false>(st, s, n16, per, n_wg, o);
 }
 
 // ------------------------------------------------------------------ allocation-free scratch

@@ -113,7 +113,8 @@ bool decode_merge_in_kernel(int chunk, int n_xcc);
 hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes);
 // the decode plan's memory traffic alone, for one sequence of len keys; sink takes one float per workgroup
 hipError_t launch_stream_ceiling(hipStream_t st, const float* kc, const float* vc, int HKV, int len, float* sink);
-hipError_t launch_read_ceiling(hipStream_t st, const void* src, size_t bytes, int n_wg, void* sink);
+hipError_t launch_read_ceiling(hipStream_t st, const void* src, size_t bytes, int n_wg, bool all_in_flight,
+                               void* sink);
 // allocation-free decode: this device's address of a static scratch array of kDecodeScratchBytes
 constexpr size_t kDecodeScratchBytes = size_t(4) << 20;
 hipError_t decode_scratch(void** ptr);

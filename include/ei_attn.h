@@ -281,10 +281,12 @@ int ei_stream_ceiling(ei_stream_t stream, const float* kc, const float* vc, int 
 /* Not part of the reference path: a plain streaming read of `bytes` (a multiple of 16, src
  * 16-byte aligned) with non-temporal 16-byte global loads by n_workgroups workgroups of 256
  * threads (1..65535, at most 64 loads per thread: bytes <= n_workgroups * 256 KiB; sink holds
- * n_workgroups * 16 bytes and is written only by chance).  Its
- * duration bounds any kernel that reads that many bytes per launch: the read ceiling a decode
- * launch of the same bytes is measured against. */
-int ei_read_ceiling(ei_stream_t stream, const void* src, size_t bytes, int n_workgroups, void* sink);
+ * n_workgroups * 16 bytes and is written only by chance).  all_in_flight != 0 issues every load of
+ * a thread before any is used; 0 lets the compiler interleave loads and uses (fewer registers,
+ * more waves).  Its duration bounds any kernel that reads that many bytes per launch: the read
+ * ceiling a decode launch of the same bytes is measured against. */
+int ei_read_ceiling(ei_stream_t stream, const void* src, size_t bytes, int n_workgroups, int all_in_flight,
+                    void* sink);
 
 /* ------------------------------------------------------------------ synthetic inputs
  * Not part of the reference path: fills n floats with the counter-based N(0,1)
