@@ -125,6 +125,28 @@ def test_qkv_project_quantised_decode_bit_exact(orc, gpu, wtype):
             assert bits_equal(g, want), f"w_type {wtype} column {c}"
 
 
+@pytest.mark.parametrize("wtype", QTYPES)
+def test_qkv_project_quantised_single_row_bit_exact(orc, gpu, wtype):
+    """The single-activation-row kernel (a wave takes its rows a pair at a time) on 70 output
+    rows, not a multiple of any workgroup's row count, so the last workgroup holds clamped rows:
+    one-hot activations at every position of a super-block, each output bit for bit the
+    reference's decoded weight times h_i."""
+    E, n_out = 1024, 70
+    gamma = orc.gamma(E, 8811)
+    blocks, wf = _qweights(orc, n_out, E, wtype, 8812 + wtype)
+    for c in range(256):
+        col = c + 256 * (c % (E // 256))
+        x = np.zeros((1, E), np.float32)
+        x[0, col] = np.float32(-2.5)
+        got = _host(_project(gpu, x, gamma, blocks, wtype, n_out))[0]
+        h = orc.rmsnorm(x[0], gamma)
+        want = (wf[:, col] * h[col]).astype(np.float32)
+        g = got.copy()
+        g[(g == 0) & (want == 0)] = 0.0  # a zero weight gives a zero of either sign
+        want[want == 0] = 0.0
+        assert bits_equal(g, want), f"w_type {wtype} column {col}"
+
+
 def test_qkv_project_rejects_unbuilt_shapes(gpu):
     import ctypes
     from exactinfer_amd import _capi
