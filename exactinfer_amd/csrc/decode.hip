@@ -270,6 +270,21 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs& a, size_t head_sl
 // NW waves per workgroup, each with a ring of kRingTiles/NW tile slots: 4 waves x 2 slots
 // streams long chunks with one tile always in flight behind the one being scored; 8 waves
 // x 1 slot gives short chunks (one tile per wave) two waves per SIMD to hide latency.
+#ifdef EI_EXP_STAMPS
+// diagnostic build only: per workgroup of the last launch, [0] device realtime at start (100 MHz),
+// [1] XCD, [2] realtime once this thread's partial store is acknowledged; k_combine from row 4096
+__device__ unsigned long long g_dstamps[8192 * 4];
+__device__ __forceinline__ unsigned long long rt_now() { return __builtin_amdgcn_s_memrealtime(); }
+__device__ __forceinline__ unsigned long long xcc_now() {
+    uint32_t x = 0;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x;
+}
+#define DSTAMP(row, i, v) do { if (threadIdx.x == 0) g_dstamps[(row) * 4 + (i)] = (v); } while (0)
+#else
+#define DSTAMP(row, i, v) do { } while (0)
+#endif
+
 template <int G, bool FUSED, int NW>
 __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     constexpr int kThreads = 64 * NW, kWaves = NW, kRing = kRingTiles / NW;
@@ -278,6 +293,8 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     constexpr int NF = NV / 8 > 0 ? NV / 8 : 1;   // finished scores per lane after xreduce8
     constexpr int NCOL = G * 32;                  // float4 columns of the G output heads
     static_assert(kRing * kTileFloats >= G * kHeadDim, "a wave's ring slots hold its partial");
+    DSTAMP(blockIdx.x, 0, rt_now());
+    DSTAMP(blockIdx.x, 1, xcc_now());
     extern __shared__ __align__(16) float ring[];          // [kWaves][kRing][kTileFloats]; later scratch
     __shared__ __align__(16) float qs[G * D];
     __shared__ __align__(16) float pw[kWaves][kTile * G];  // per wave: p[row][g] of the current tile
@@ -627,6 +644,10 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     if (!merging) {  // k_combine merges in a second launch and reads only the (m, l) words of real heads
         if (tid < NCOL && d4 == 0 && gcol < Gr)
             *reinterpret_cast<float2*>(my_rec + 2 + 2 * gcol) = make_float2(Mw, Lw);
+#ifdef EI_EXP_STAMPS
+        wait_vmcnt<0>();
+        DSTAMP(blockIdx.x, 2, rt_now());
+#endif
         return;
     }
     __shared__ float mlsh[2 * G];
@@ -688,6 +709,8 @@ template <int G>
 __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
     constexpr int D = kHeadDim, B = 32, NA = 4, KM = kDecodeMaxSplits / 64;
     __shared__ float wsh[kDecodeMaxSplits];
+    DSTAMP(4096 + blockIdx.x, 0, rt_now());
+    DSTAMP(4096 + blockIdx.x, 1, xcc_now());
     __shared__ float Lsh;
     const int hq = blockIdx.x % a.H, seq = blockIdx.x / a.H;
     const int Gr = a.H / a.HKV;  // partials are laid out with G (>= Gr) head slots
@@ -739,6 +762,10 @@ __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
     }
     const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     a.out[(size_t)seq * a.H * D + (size_t)hq * D + tid] = Lsh > 0.f ? sum / Lsh : 0.f;  // kv_len 0: zeros
+#ifdef EI_EXP_STAMPS
+    wait_vmcnt<0>();
+    DSTAMP(4096 + blockIdx.x, 2, rt_now());
+#endif
 }
 
 __global__ void k_ws_clear(uint32_t* p, size_t n) {
@@ -988,3 +1015,9 @@ hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes) {
 }
 
 }  // namespace ei
+
+#ifdef EI_EXP_STAMPS
+extern "C" __attribute__((visibility("default"))) int ei_diag_decode_stamps(void* host, size_t n) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ei::g_dstamps), n * 8, 0, hipMemcpyDeviceToHost);
+}
+#endif
