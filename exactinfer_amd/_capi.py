@@ -77,6 +77,9 @@ _SIGS = {
 _lib = None
 
 
+ABI_VERSION = 3  # EI_ABI_VERSION of include/ei_attn.h
+
+
 class EiError(RuntimeError):
     """A non-zero status from the C ABI (the reference raises std::runtime_error)."""
 
@@ -96,6 +99,9 @@ def lib() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = res
+        if L.ei_abi_version() != ABI_VERSION:  # the signatures above are those of this revision
+            raise RuntimeError(f"{LIB_PATH} has ABI version {L.ei_abi_version()}, this binding expects "
+                               f"{ABI_VERSION}: rebuild the library")
         _lib = L
     return _lib
 

@@ -85,7 +85,7 @@ int check_rope_fused_decode(int rope_dim, int head_dim) {
 
 EI_API const char* ei_last_error(void) { return g_err.c_str(); }
 
-EI_API int ei_abi_version(void) { return 3; }
+EI_API int ei_abi_version(void) { return EI_ABI_VERSION; }
 
 EI_API int ei_rope_table_fill(float* cs_host, int n_ctx, int rope_dim, double theta) {
     REQUIRE(cs_host != nullptr, "cs_host is null");

@@ -47,7 +47,8 @@ enum {
 /* Message of the last failure on this thread ("" if none).  Valid until the next call. */
 const char* ei_last_error(void);
 
-/* ABI version, bumped on any signature change. */
+/* ABI version, bumped on any signature change: a host checks ei_abi_version() == EI_ABI_VERSION. */
+#define EI_ABI_VERSION 3
 int ei_abi_version(void);
 
 /* ------------------------------------------------------------------ RoPE table

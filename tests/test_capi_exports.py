@@ -30,7 +30,8 @@ def test_library_exports_every_declared_symbol():
     L = _capi.lib()
     for name in _declared():
         assert isinstance(getattr(L, name), ctypes._CFuncPtr), name
-    assert L.ei_abi_version() == 3
+    header = int(re.search(r"#define EI_ABI_VERSION (\d+)", (ROOT / "include" / "ei_attn.h").read_text()).group(1))
+    assert L.ei_abi_version() == header == _capi.ABI_VERSION == 3
 
 
 def test_rope_table_fill_host_matches_oracle(orc):
