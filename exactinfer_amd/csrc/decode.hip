@@ -271,18 +271,35 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs& a, size_t head_sl
 // streams long chunks with one tile always in flight behind the one being scored; 8 waves
 // x 1 slot gives short chunks (one tile per wave) two waves per SIMD to hide latency.
 #ifdef EI_EXP_STAMPS
-// diagnostic build only: per workgroup of the last launch, [0] device realtime at start (100 MHz),
-// [1] XCD, [2] realtime once this thread's partial store is acknowledged; k_combine from row 4096
+// Diagnostic build only.  Per workgroup of the last launch: [0] device realtime at start (100 MHz,
+// common to all XCDs), [1] XCD, [2] realtime once this thread's partial (k_combine: output) store
+// is acknowledged; k_combine's rows from 4096.  Per launch, block 0's start time in a ring of 1024
+// ([0] k_decode, [1] k_combine).  Nothing is stored before the workgroup's end: a store issued
+// early counts in vmcnt and would hold up the waits that follow it.
 __device__ unsigned long long g_dstamps[8192 * 4];
+__device__ unsigned long long g_dlaunch[2][1024];
+__device__ unsigned g_dctr[2];
 __device__ __forceinline__ unsigned long long rt_now() { return __builtin_amdgcn_s_memrealtime(); }
 __device__ __forceinline__ unsigned long long xcc_now() {
     uint32_t x = 0;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
     return x;
 }
-#define DSTAMP(row, i, v) do { if (threadIdx.x == 0) g_dstamps[(row) * 4 + (i)] = (v); } while (0)
+__device__ __forceinline__ void stamps_store(unsigned row, int kernel, unsigned long long t0, unsigned long long xcc) {
+    wait_vmcnt<0>();
+    const unsigned long long t1 = rt_now();
+    if (threadIdx.x == 0) {
+        g_dstamps[row * 4 + 0] = t0;
+        g_dstamps[row * 4 + 1] = xcc;
+        g_dstamps[row * 4 + 2] = t1;
+        if (blockIdx.x == 0) g_dlaunch[kernel][atomicAdd(&g_dctr[kernel], 1u) & 1023u] = t0;
+    }
+}
+#define STAMP_BEGIN const unsigned long long st_t0 = rt_now(), st_xcc = xcc_now()
+#define STAMP_END(row, kernel) stamps_store((row), (kernel), st_t0, st_xcc)
 #else
-#define DSTAMP(row, i, v) do { } while (0)
+#define STAMP_BEGIN do { } while (0)
+#define STAMP_END(row, kernel) do { } while (0)
 #endif
 
 template <int G, bool FUSED, int NW>
@@ -293,8 +310,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     constexpr int NF = NV / 8 > 0 ? NV / 8 : 1;   // finished scores per lane after xreduce8
     constexpr int NCOL = G * 32;                  // float4 columns of the G output heads
     static_assert(kRing * kTileFloats >= G * kHeadDim, "a wave's ring slots hold its partial");
-    DSTAMP(blockIdx.x, 0, rt_now());
-    DSTAMP(blockIdx.x, 1, xcc_now());
+    STAMP_BEGIN;
     extern __shared__ __align__(16) float ring[];          // [kWaves][kRing][kTileFloats]; later scratch
     __shared__ __align__(16) float qs[G * D];
     __shared__ __align__(16) float pw[kWaves][kTile * G];  // per wave: p[row][g] of the current tile
@@ -644,10 +660,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode(const DecodeArgs a) {
     if (!merging) {  // k_combine merges in a second launch and reads only the (m, l) words of real heads
         if (tid < NCOL && d4 == 0 && gcol < Gr)
             *reinterpret_cast<float2*>(my_rec + 2 + 2 * gcol) = make_float2(Mw, Lw);
-#ifdef EI_EXP_STAMPS
-        wait_vmcnt<0>();
-        DSTAMP(blockIdx.x, 2, rt_now());
-#endif
+        STAMP_END(blockIdx.x, 0);
         return;
     }
     __shared__ float mlsh[2 * G];
@@ -709,8 +722,7 @@ template <int G>
 __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
     constexpr int D = kHeadDim, B = 32, NA = 4, KM = kDecodeMaxSplits / 64;
     __shared__ float wsh[kDecodeMaxSplits];
-    DSTAMP(4096 + blockIdx.x, 0, rt_now());
-    DSTAMP(4096 + blockIdx.x, 1, xcc_now());
+    STAMP_BEGIN;
     __shared__ float Lsh;
     const int hq = blockIdx.x % a.H, seq = blockIdx.x / a.H;
     const int Gr = a.H / a.HKV;  // partials are laid out with G (>= Gr) head slots
@@ -762,10 +774,7 @@ __global__ __launch_bounds__(128) void k_combine(const DecodeArgs a) {
     }
     const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     a.out[(size_t)seq * a.H * D + (size_t)hq * D + tid] = Lsh > 0.f ? sum / Lsh : 0.f;  // kv_len 0: zeros
-#ifdef EI_EXP_STAMPS
-    wait_vmcnt<0>();
-    DSTAMP(4096 + blockIdx.x, 2, rt_now());
-#endif
+    STAMP_END(4096 + blockIdx.x, 1);
 }
 
 __global__ void k_ws_clear(uint32_t* p, size_t n) {
@@ -1017,6 +1026,9 @@ hipError_t launch_ws_clear(hipStream_t st, void* ws, size_t bytes) {
 }  // namespace ei
 
 #ifdef EI_EXP_STAMPS
+extern "C" __attribute__((visibility("default"))) int ei_diag_decode_launches(void* host) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ei::g_dlaunch), sizeof(ei::g_dlaunch), 0, hipMemcpyDeviceToHost);
+}
 extern "C" __attribute__((visibility("default"))) int ei_diag_decode_stamps(void* host, size_t n) {
     return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(ei::g_dstamps), n * 8, 0, hipMemcpyDeviceToHost);
 }
